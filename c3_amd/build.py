@@ -1,0 +1,85 @@
+"""Build recipe for the gfx950 backend (no cmake needed).
+
+Products, all in-tree under c3_amd/lib/ (git-ignored, shipped with the tree):
+  *.hsaco        gfx950 code objects, one per kernel family (hipcc --genco)
+  libc3hip.so    host C-ABI library (include/c3hip.h) that loads them
+  libc3core.so   C++ dispatch layer (registry, hot-path manager, JIT cache)
+  c3core_tests   C++ unit-test runner for the dispatch layer (CPU only)
+and the oracle (test infrastructure) under oracle/liboracle.so.
+
+Run:  python -m c3_amd.build   (or __graft_entry__.build()).
+"""
+from __future__ import annotations
+
+import os
+import shlex
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent.parent
+PKG = ROOT / "c3_amd"
+CSRC = PKG / "csrc"
+LIB = PKG / "lib"
+INCLUDE = ROOT / "include"
+ORACLE = ROOT / "oracle"
+
+ARCH = "gfx950"
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+# Packed fp32 ops stay off in all device code; hipcc would otherwise form
+# v_pk_* fp32 instructions from ordinary float code.
+NO_PACKED_FP32 = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+DEVICE_FLAGS = ["--genco", "--no-gpu-bundle-output", f"--offload-arch={ARCH}", "-O3", "-std=c++17", *NO_PACKED_FP32]
+
+KERNELS = ["elementwise", "gemm_f32", "reduce"]
+RUNTIME_SOURCES = ["runtime/c3hip_runtime.cpp", "runtime/c3hip_ops.cpp"]
+
+
+def _run(cmd: list[str], cwd: Path | None = None) -> None:
+    proc = subprocess.run(cmd, cwd=cwd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if proc.returncode != 0:
+        sys.stderr.write(proc.stdout)
+        raise RuntimeError(f"build step failed ({proc.returncode}): {shlex.join(cmd)}")
+
+
+def build_code_objects() -> list[Path]:
+    LIB.mkdir(parents=True, exist_ok=True)
+    jobs = []
+    for k in KERNELS:
+        src = CSRC / "kernels" / f"{k}.hip"
+        out = LIB / f"{k}.hsaco"
+        jobs.append(([HIPCC, *DEVICE_FLAGS, f"-I{CSRC / 'kernels'}", str(src), "-o", str(out)], out))
+    with ThreadPoolExecutor(max_workers=min(4, len(jobs))) as ex:
+        list(ex.map(lambda j: _run(j[0]), jobs))
+    return [j[1] for j in jobs]
+
+
+def build_runtime() -> Path:
+    out = LIB / "libc3hip.so"
+    srcs = [str(CSRC / s) for s in RUNTIME_SOURCES]
+    # Host-only C++: no device code in these files, so hipcc only supplies the
+    # HIP headers and links libamdhip64.
+    cmd = [HIPCC, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", f"-I{INCLUDE}", f"-I{CSRC / 'runtime'}",
+           *srcs, "-o", str(out), "-ldl"]
+    _run(cmd)
+    return out
+
+
+def build_oracle() -> Path:
+    _run(["make", "-s", "-C", str(ORACLE), "liboracle.so"])
+    return ORACLE / "liboracle.so"
+
+
+def build_all(verbose: bool = False) -> None:
+    built = []
+    built += build_code_objects()
+    built.append(build_runtime())
+    built.append(build_oracle())
+    if verbose:
+        for b in built:
+            print(f"built {b.relative_to(ROOT)} ({b.stat().st_size} bytes)")
+
+
+if __name__ == "__main__":
+    build_all(verbose=True)

@@ -1,0 +1,105 @@
+// elementwise.hip -- the eight single-node elementwise ops as HBM streams.
+//
+// Reference ops (fp32, one IEEE operation per element):
+//   add/sub/mul/div : BinaryOpLowering, src/C3/C3DialectLowering.cpp:246-291
+//                     (bmod > 0: rhs index = idx mod bmod)
+//   neg             : UnaryOpLowering<NegOp> (arith.negf), :294-317
+//   relu            : ReLUOpLowering, maxnumf(x, 0), :319-350
+//   scale           : Mul by a scalar (LinalgElementwiseGen rhs_mod = 1,
+//                     src/C3/LinalgElementwiseGen.cpp:168-186)
+//   relu_bwd        : Gt(z, 0) then Mul(mask, grad),
+//                     src/C3/C3BackwardCapture.cpp:501-528 + src/C3/MLIRKernelGen.cpp:173-211
+//
+// Layout: flat contiguous fp32 arrays.  Fast path: 16-byte vectors, UNROLL
+// vectors per thread issued back to back so each wave keeps several KiB in
+// flight, non-temporal hints (the data is touched once).  The host picks the
+// scalar kernel when n or a base address is not 16-byte friendly.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+enum { EW_ADD = 0, EW_SUB = 1, EW_MUL = 2, EW_DIV = 3, EW_RELU = 4, EW_RELU_BWD = 5, EW_NEG = 6, EW_SCALE = 7 };
+
+template <int OP>
+__device__ __forceinline__ float ew_apply(float a, float b, float alpha) {
+    if (OP == EW_ADD) return a + b;
+    if (OP == EW_SUB) return a - b;
+    if (OP == EW_MUL) return a * b;
+    if (OP == EW_DIV) return a / b;              // IEEE correctly rounded division
+    if (OP == EW_RELU) return fmaxf(a, 0.0f);    // maxnum: NaN -> 0
+    if (OP == EW_RELU_BWD) return (a > 0.0f ? 1.0f : 0.0f) * b;
+    if (OP == EW_NEG) return -a;
+    return a * alpha;                            // EW_SCALE
+}
+
+template <int OP>
+constexpr bool ew_binary() {
+    return OP == EW_ADD || OP == EW_SUB || OP == EW_MUL || OP == EW_DIV || OP == EW_RELU_BWD;
+}
+
+constexpr int kThreads = 256;
+constexpr int kUnroll = 4;
+
+__device__ __forceinline__ f32x4 ld_nt(const f32x4* p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ void st_nt(f32x4 v, f32x4* p) { __builtin_nontemporal_store(v, p); }
+
+// Vector kernel: n4 = number of float4 vectors; bmod4 = bmod / 4 (0 = no broadcast).
+template <int OP>
+__device__ __forceinline__ void ew_vec_body(const f32x4* __restrict__ a, const f32x4* __restrict__ b,
+                                            float alpha, f32x4* __restrict__ out, int64_t n4, int64_t bmod4) {
+    const int64_t base = (int64_t)blockIdx.x * (kThreads * kUnroll) + threadIdx.x;
+    f32x4 va[kUnroll], vb[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const int64_t i = base + (int64_t)u * kThreads;
+        if (i < n4) {
+            va[u] = ld_nt(a + i);
+            if (ew_binary<OP>()) vb[u] = bmod4 > 0 ? b[i % bmod4] : ld_nt(b + i);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const int64_t i = base + (int64_t)u * kThreads;
+        if (i < n4) {
+            f32x4 r;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) r[e] = ew_apply<OP>(va[u][e], ew_binary<OP>() ? vb[u][e] : 0.0f, alpha);
+            st_nt(r, out + i);
+        }
+    }
+}
+
+// Scalar kernel: any n, any alignment, bmod > 0 broadcasts rhs, bmod < 0 broadcasts lhs.
+template <int OP>
+__device__ __forceinline__ void ew_scalar_body(const float* __restrict__ a, const float* __restrict__ b,
+                                               float alpha, float* __restrict__ out, int64_t n, int64_t bmod) {
+    const int64_t stride = (int64_t)gridDim.x * kThreads;
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += stride) {
+        int64_t li = i, ri = i;
+        if (bmod > 0) ri = i % bmod;
+        else if (bmod < 0) li = i % (-bmod);
+        const float x = a[li];
+        const float y = ew_binary<OP>() ? b[ri] : 0.0f;
+        out[i] = ew_apply<OP>(x, y, alpha);
+    }
+}
+
+#define C3_EW(NAME, OP)                                                                                  \
+    extern "C" __global__ __launch_bounds__(kThreads) void c3_ew_##NAME##_f32_v(                       \
+        const f32x4* a, const f32x4* b, float alpha, f32x4* out, int64_t n4, int64_t bmod4) {          \
+        ew_vec_body<OP>(a, b, alpha, out, n4, bmod4);                                                   \
+    }                                                                                                   \
+    extern "C" __global__ __launch_bounds__(kThreads) void c3_ew_##NAME##_f32_s(                       \
+        const float* a, const float* b, float alpha, float* out, int64_t n, int64_t bmod) {            \
+        ew_scalar_body<OP>(a, b, alpha, out, n, bmod);                                                  \
+    }
+
+C3_EW(add, EW_ADD)
+C3_EW(sub, EW_SUB)
+C3_EW(mul, EW_MUL)
+C3_EW(div, EW_DIV)
+C3_EW(relu, EW_RELU)
+C3_EW(relu_bwd, EW_RELU_BWD)
+C3_EW(neg, EW_NEG)
+C3_EW(scale, EW_SCALE)

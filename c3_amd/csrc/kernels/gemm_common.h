@@ -1,0 +1,69 @@
+// gemm_common.h -- shared definitions for the gfx950 GEMM code objects.
+//
+// Logical problem: C[M,N] = sum_k A(m,k) * B(k,n), fp32 accumulation.
+//   A(m,k) lives at A[m*lda + k] when the operand is "k-contiguous" (AK),
+//   else at A[k*lda + m].  B(k,n) lives at B[n*ldb + k] when k-contiguous
+//   (BKC), else at B[k*ldb + n].
+// The three GEMMs of one Linear layer map onto this as
+//   forward  Y  = X . W      : A = X  (AK),      B = W (row-major [K,N], !BKC)
+//   backward dX = dZ . W^T   : A = dZ (AK),      B = W (BKC: B(k=n, j) = W[j*N+n])
+//   backward dW = X^T . dZ   : A = X  (!AK),     B = dZ (!BKC)
+// where dZ = (Y > 0 ? 1 : 0) * dY is formed while the tile is loaded
+// (mask prologue), never materialised in HBM.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+struct GemmArgs {
+    const void* A;      // operand A (fp32 or bf16)
+    const void* Amask;  // mask source with A's layout (Y of the forward), or null
+    const void* B;
+    const void* Bmask;
+    void* C;            // output [M, ldc]
+    const float* bias;  // per-column bias (fp32), or null
+    float* db;          // column sums of the masked B operand over k (fp32), or null
+    int64_t M, N, K;
+    int64_t lda, ldb, ldc;
+    int act;            // 0: none, 1: ReLU (maxnum(x, 0))
+    int _pad;
+};
+
+// Blocks are handed to the 8 XCDs round-robin (block i runs on XCD i % 8).
+// Renumber so that consecutive logical tiles land on the same XCD and share
+// its L2, then walk tiles in groups of GROUP_M row-tiles so that a group's
+// A rows and B columns stay L2-resident.
+template <int GROUP_M>
+__device__ __forceinline__ void tile_coords(int64_t M, int64_t N, int BM, int BN, int& tm, int& tn) {
+    const int nbm = (int)((M + BM - 1) / BM);
+    const int nbn = (int)((N + BN - 1) / BN);
+    const int nblk = nbm * nbn;
+    int bid = blockIdx.x;
+    int id = bid;
+    if ((nblk & 7) == 0) id = (bid & 7) * (nblk >> 3) + (bid >> 3);
+    const int per_group = GROUP_M * nbn;
+    const int g = id / per_group;
+    const int first_m = g * GROUP_M;
+    const int gsz = min(nbm - first_m, GROUP_M);
+    const int r = id - g * per_group;
+    tm = first_m + r % gsz;
+    tn = r / gsz;
+}
+
+__device__ __forceinline__ float relu_mask(float y) { return y > 0.0f ? 1.0f : 0.0f; }
+
+// maxnum(x, 0): NaN -> 0 (llvm.maxnum semantics, v_max_f32).
+__device__ __forceinline__ float act_apply(float v, int act) { return act == 1 ? fmaxf(v, 0.0f) : v; }
+
+__device__ __forceinline__ unsigned short f32_to_bf16_rne(float x) {
+    uint32_t u = __float_as_uint(x);
+    if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (unsigned short)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (unsigned short)(u >> 16);
+}
+
+__device__ __forceinline__ float bf16_to_f32(unsigned short h) { return __uint_as_float(((uint32_t)h) << 16); }

@@ -1,0 +1,73 @@
+// reduce.hip -- SumReduce of a row-major [M, N] fp32 matrix.
+//
+// Reference: SumReduceOpLowering, src/C3/C3DialectLowering.cpp:382-465.
+//   axis 0: out[j] = sum_i in[i*N + j]   (the bias gradient db, Add backward
+//           input 1, src/C3/C3BackwardCapture.cpp:618-644, axis from :1641-1700)
+//   axis 1: out[i] = sum_j in[i*N + j]
+// The reference sums sequentially from 0.0f; here the sum is split into row
+// chunks (axis 0) or lane strides (axis 1) and combined in a fixed order, so
+// the result is deterministic run to run and within fp32 rounding of the
+// sequential sum.
+//
+// axis 0 is two passes: pass 1 writes one partial row per chunk of rows into
+// a workspace [nchunks, N]; pass 2 adds the partials in chunk order.  Each
+// thread owns one column, so every row access of a wave is 256 contiguous
+// bytes.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+constexpr int kThreads = 256;
+
+// mask (nullable, same layout as in): sums (mask > 0 ? 1 : 0) * in, the bias
+// gradient of a ReLU layer computed from its forward output Y and dY.
+extern "C" __global__ __launch_bounds__(kThreads) void c3_colsum_partial_f32(
+    const float* __restrict__ in, const float* __restrict__ mask, float* __restrict__ part, int64_t M, int64_t N,
+    int64_t rows_per_chunk) {
+    const int64_t j = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    const int64_t chunk = blockIdx.y;
+    if (j >= N) return;
+    const int64_t r0 = chunk * rows_per_chunk;
+    const int64_t r1 = min(M, r0 + rows_per_chunk);
+    // Four independent partial sums for memory-level parallelism, combined in
+    // a fixed order.
+    float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    int64_t i = r0;
+    if (mask) {
+        for (; i + 4 <= r1; i += 4)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int64_t o = (i + q) * N + j;
+                s[q] += (mask[o] > 0.0f ? 1.0f : 0.0f) * in[o];
+            }
+        for (; i < r1; ++i) s[0] += (mask[i * N + j] > 0.0f ? 1.0f : 0.0f) * in[i * N + j];
+    } else {
+        for (; i + 4 <= r1; i += 4)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) s[q] += in[(i + q) * N + j];
+        for (; i < r1; ++i) s[0] += in[i * N + j];
+    }
+    part[chunk * N + j] = (s[0] + s[1]) + (s[2] + s[3]);
+}
+
+extern "C" __global__ __launch_bounds__(kThreads) void c3_colsum_final_f32(
+    const float* __restrict__ part, float* __restrict__ out, int64_t nchunks, int64_t N) {
+    const int64_t j = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (j >= N) return;
+    float s = 0.0f;
+    for (int64_t c = 0; c < nchunks; ++c) s += part[c * N + j];
+    out[j] = s;
+}
+
+// One wave per row.
+extern "C" __global__ __launch_bounds__(kThreads) void c3_rowsum_f32(
+    const float* __restrict__ in, float* __restrict__ out, int64_t M, int64_t N) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    if (row >= M) return;
+    const float* p = in + row * N;
+    float s = 0.0f;
+    for (int64_t j = lane; j < N; j += 64) s += p[j];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
+    if (lane == 0) out[row] = s;
+}

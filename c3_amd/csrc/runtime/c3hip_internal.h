@@ -1,0 +1,43 @@
+// c3hip_internal.h -- shared helpers of the C-ABI implementation files.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+namespace c3hip {
+
+// Record `msg` as the calling thread's last error and return `code`.
+int set_error(int code, const std::string& msg);
+void clear_error();
+const char* last_error();
+
+int current_device(int* dev);
+int init_device(int device);
+int shutdown_all();
+
+// Resolve `name` in the current device's code objects (loading them on first use).
+int get_function(const char* name, hipFunction_t* fn);
+
+// hipModuleLaunchKernel of kernel `name` with the kernelParams array `args`.
+int launch(const char* name, dim3 grid, dim3 block, void** args, hipStream_t stream);
+
+// Kernel argument block of every GEMM code object (mirrors GemmArgs in
+// c3_amd/csrc/kernels/gemm_common.h; both sides are plain C layout).
+struct GemmArgs {
+    const void* A;
+    const void* Amask;
+    const void* B;
+    const void* Bmask;
+    void* C;
+    const float* bias;
+    float* db;
+    int64_t M, N, K;
+    int64_t lda, ldb, ldc;
+    int act;
+    int _pad;
+};
+
+inline bool aligned16(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace c3hip

@@ -1,0 +1,275 @@
+// c3hip_ops.cpp -- argument checking and kernel selection behind the compute
+// entry points of include/c3hip.h.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+
+#include "c3hip.h"
+#include "c3hip_internal.h"
+
+namespace c3hip {
+namespace {
+
+constexpr int64_t kMaxElems32 = (int64_t)1 << 32;  // GEMM operands use 32-bit element offsets
+
+const char* ew_name(int op) {
+    switch (op) {
+        case C3HIP_EW_ADD: return "add";
+        case C3HIP_EW_SUB: return "sub";
+        case C3HIP_EW_MUL: return "mul";
+        case C3HIP_EW_DIV: return "div";
+        case C3HIP_EW_RELU: return "relu";
+        case C3HIP_EW_RELU_BWD: return "relu_bwd";
+        case C3HIP_EW_NEG: return "neg";
+        case C3HIP_EW_SCALE: return "scale";
+        default: return nullptr;
+    }
+}
+
+bool ew_is_binary(int op) {
+    return op == C3HIP_EW_ADD || op == C3HIP_EW_SUB || op == C3HIP_EW_MUL || op == C3HIP_EW_DIV ||
+           op == C3HIP_EW_RELU_BWD;
+}
+
+// ---- GEMM planning -------------------------------------------------------
+
+enum class Kind { Fwd, Dx, DxMask, Dw, DwMask, TT };
+
+const char* kind_name(Kind k) {
+    switch (k) {
+        case Kind::Fwd: return "fwd";
+        case Kind::Dx: return "dx";
+        case Kind::DxMask: return "dx_mask";
+        case Kind::Dw: return "dw";
+        case Kind::DwMask: return "dw_mask";
+        case Kind::TT: return "tt";
+    }
+    return "?";
+}
+
+struct Tile {
+    const char* name;
+    int bm, bn, threads;
+};
+
+const Tile kF32Tiles[] = {{"t64x64", 64, 64, 256}, {"t128x128", 128, 128, 256}, {"t256x128", 256, 128, 512}};
+
+const Tile* find_tile(const Tile* tiles, size_t n, const char* name) {
+    for (size_t i = 0; i < n; ++i)
+        if (std::strcmp(tiles[i].name, name) == 0) return &tiles[i];
+    return nullptr;
+}
+
+// Tile choice: the large tile once it yields at least two blocks per CU on
+// MI355X's 256 CUs, else the 64x64 tile (small layers are latency-bound).
+// C3_HIP_GEMM_TILE overrides (benchmark sweeps).
+const Tile* choose_f32_tile(int64_t M, int64_t N) {
+    const size_t nt = sizeof(kF32Tiles) / sizeof(kF32Tiles[0]);
+    if (const char* env = std::getenv("C3_HIP_GEMM_TILE")) {
+        if (const Tile* t = find_tile(kF32Tiles, nt, env)) return t;
+    }
+    const int64_t blocks128 = ((M + 127) / 128) * ((N + 127) / 128);
+    if (blocks128 >= 512) return &kF32Tiles[1];
+    return &kF32Tiles[0];
+}
+
+// Can an operand use 16-byte vector loads?  kc: k is its contiguous index.
+bool vec_ok(bool kc, int64_t rows, int64_t k, int64_t ld, const void* p, const void* pm) {
+    if (ld % 4 != 0) return false;
+    if (kc ? (k % 4 != 0) : (rows % 4 != 0)) return false;
+    return aligned16(p) && aligned16(pm);
+}
+
+int run_gemm(int dtype, Kind kind, const GemmArgs& a0, bool a_kc, bool b_kc, hipStream_t stream) {
+    GemmArgs a = a0;
+    if (a.M == 0 || a.N == 0) return C3HIP_OK;
+    if (dtype != C3HIP_F32) return set_error(C3HIP_ERR_UNSUPPORTED, "bf16 GEMM kernels are not built in this library");
+    const Tile* t = choose_f32_tile(a.M, a.N);
+    const bool vec = vec_ok(a_kc, a.M, a.K, a.lda, a.A, a.Amask) && vec_ok(b_kc, a.N, a.K, a.ldb, a.B, a.Bmask);
+    char name[96];
+    std::snprintf(name, sizeof(name), "c3_gemm_f32_%s_%s_%s", kind_name(kind), t->name, vec ? "v" : "s");
+    const int64_t blocks = ((a.M + t->bm - 1) / t->bm) * ((a.N + t->bn - 1) / t->bn);
+    if (blocks > 0x7fffffff) return set_error(C3HIP_ERR_TOO_LARGE, "GEMM grid too large");
+    void* args[] = {&a};
+    return launch(name, dim3((unsigned)blocks), dim3(t->threads), args, stream);
+}
+
+int check_elems(const char* what, int64_t rows, int64_t cols) {
+    if (rows < 0 || cols < 0) return set_error(C3HIP_ERR_INVALID, std::string(what) + ": negative dimension");
+    if (cols > 0 && rows > (kMaxElems32 - 1) / cols)
+        return set_error(C3HIP_ERR_TOO_LARGE, std::string(what) + ": more than 2^32 elements");
+    return C3HIP_OK;
+}
+
+int check_dtype(int dtype) {
+    if (dtype != C3HIP_F32 && dtype != C3HIP_BF16) return set_error(C3HIP_ERR_INVALID, "unknown dtype " + std::to_string(dtype));
+    return C3HIP_OK;
+}
+
+// Column sums of (optionally masked) fp32 [M,N] into out[N]: one pass when M
+// is small, else per-chunk partials in a stream-ordered workspace.
+int colsum(const float* in, const float* mask, float* out, int64_t M, int64_t N, hipStream_t stream) {
+    if (N == 0) return C3HIP_OK;
+    const int64_t kChunk = 256;
+    int64_t nchunks = (M + kChunk - 1) / kChunk;
+    if (nchunks < 1) nchunks = 1;
+    if (nchunks > 64) nchunks = 64;
+    int64_t rows_per_chunk = (M + nchunks - 1) / nchunks;
+    if (rows_per_chunk < 1) rows_per_chunk = 1;
+    const unsigned gx = (unsigned)((N + 255) / 256);
+    const char* pname = "c3_colsum_partial_f32";
+    if (nchunks == 1) {
+        void* args[] = {(void*)&in, (void*)&mask, (void*)&out, &M, &N, &rows_per_chunk};
+        return launch(pname, dim3(gx, 1), dim3(256), args, stream);
+    }
+    float* part = nullptr;
+    hipError_t e = hipMallocAsync((void**)&part, (size_t)(nchunks * N) * sizeof(float), stream);
+    if (e != hipSuccess) return set_error(C3HIP_ERR_HIP, std::string("hipMallocAsync failed: ") + hipGetErrorString(e));
+    void* args1[] = {(void*)&in, (void*)&mask, (void*)&part, &M, &N, &rows_per_chunk};
+    int rc = launch(pname, dim3(gx, (unsigned)nchunks), dim3(256), args1, stream);
+    if (rc == C3HIP_OK) {
+        void* args2[] = {(void*)&part, (void*)&out, &nchunks, &N};
+        rc = launch("c3_colsum_final_f32", dim3(gx), dim3(256), args2, stream);
+    }
+    e = hipFreeAsync(part, stream);
+    if (rc == C3HIP_OK && e != hipSuccess)
+        rc = set_error(C3HIP_ERR_HIP, std::string("hipFreeAsync failed: ") + hipGetErrorString(e));
+    return rc;
+}
+
+}  // namespace
+}  // namespace c3hip
+
+using namespace c3hip;
+
+extern "C" {
+
+int c3hip_elementwise(int op, int dtype, const void* a, const void* b, float alpha, void* out, int64_t n,
+                      int64_t bmod, void* stream_) {
+    clear_error();
+    hipStream_t stream = (hipStream_t)stream_;
+    const char* nm = ew_name(op);
+    if (!nm) return set_error(C3HIP_ERR_INVALID, "unknown elementwise op " + std::to_string(op));
+    int rc = check_dtype(dtype);
+    if (rc) return rc;
+    if (dtype != C3HIP_F32) return set_error(C3HIP_ERR_UNSUPPORTED, "elementwise ops take fp32 only");
+    if (n < 0) return set_error(C3HIP_ERR_INVALID, "n < 0");
+    if (n == 0) return C3HIP_OK;
+    const bool binary = ew_is_binary(op);
+    if (!a || !out || (binary && !b)) return set_error(C3HIP_ERR_INVALID, "null pointer");
+    if (bmod == n) bmod = 0;
+    if (!binary && bmod > 0) bmod = 0;
+    char name[64];
+    const bool vec = (n % 4 == 0) && aligned16(a) && aligned16(out) && (bmod >= 0) &&
+                     (!binary || (aligned16(b) && (bmod == 0 || bmod % 4 == 0)));
+    if (vec) {
+        std::snprintf(name, sizeof(name), "c3_ew_%s_f32_v", nm);
+        int64_t n4 = n / 4, bmod4 = bmod / 4;
+        const int64_t per_block = 256 * 4;
+        const int64_t blocks = (n4 + per_block - 1) / per_block;
+        if (blocks > 0x7fffffff) return set_error(C3HIP_ERR_TOO_LARGE, "elementwise grid too large");
+        void* args[] = {(void*)&a, (void*)&b, &alpha, &out, &n4, &bmod4};
+        return launch(name, dim3((unsigned)blocks), dim3(256), args, stream);
+    }
+    std::snprintf(name, sizeof(name), "c3_ew_%s_f32_s", nm);
+    const int64_t blocks = std::min<int64_t>((n + 255) / 256, 1 << 16);
+    void* args[] = {(void*)&a, (void*)&b, &alpha, &out, &n, &bmod};
+    return launch(name, dim3((unsigned)blocks), dim3(256), args, stream);
+}
+
+int c3hip_matmul(int dtype, const void* A, const void* B, void* C, int64_t M, int64_t K, int64_t N, int transA,
+                 int transB, void* stream) {
+    clear_error();
+    int rc = check_dtype(dtype);
+    if (rc) return rc;
+    if ((rc = check_elems("A", M, K)) || (rc = check_elems("B", K, N)) || (rc = check_elems("C", M, N))) return rc;
+    if (M > 0 && N > 0 && (!C || (K > 0 && (!A || !B)))) return set_error(C3HIP_ERR_INVALID, "null pointer");
+    GemmArgs a{};
+    a.A = A; a.B = B; a.C = C;
+    a.M = M; a.N = N; a.K = K;
+    a.lda = transA ? M : K;
+    a.ldb = transB ? K : N;
+    a.ldc = N;
+    a.act = C3HIP_ACT_NONE;
+    const bool a_kc = !transA, b_kc = transB != 0;
+    Kind kind = !transA ? (transB ? Kind::Dx : Kind::Fwd) : (transB ? Kind::TT : Kind::Dw);
+    return run_gemm(dtype, kind, a, a_kc, b_kc, (hipStream_t)stream);
+}
+
+int c3hip_linear_fwd(int dtype, const void* X, const void* W, const float* b, void* Y, int64_t M, int64_t K,
+                     int64_t N, int act, void* stream) {
+    clear_error();
+    int rc = check_dtype(dtype);
+    if (rc) return rc;
+    if (act != C3HIP_ACT_NONE && act != C3HIP_ACT_RELU) return set_error(C3HIP_ERR_INVALID, "unknown act");
+    if ((rc = check_elems("X", M, K)) || (rc = check_elems("W", K, N)) || (rc = check_elems("Y", M, N))) return rc;
+    if (M > 0 && N > 0 && (!Y || (K > 0 && (!X || !W)))) return set_error(C3HIP_ERR_INVALID, "null pointer");
+    GemmArgs a{};
+    a.A = X; a.B = W; a.C = Y; a.bias = b;
+    a.M = M; a.N = N; a.K = K;
+    a.lda = K; a.ldb = N; a.ldc = N;
+    a.act = act;
+    return run_gemm(dtype, Kind::Fwd, a, true, false, (hipStream_t)stream);
+}
+
+int c3hip_linear_bwd(int dtype, const void* X, const void* W, const void* Y, const void* dY, void* dX, float* dW,
+                     float* db, int64_t M, int64_t K, int64_t N, int act, void* stream_) {
+    clear_error();
+    hipStream_t stream = (hipStream_t)stream_;
+    int rc = check_dtype(dtype);
+    if (rc) return rc;
+    if (act != C3HIP_ACT_NONE && act != C3HIP_ACT_RELU) return set_error(C3HIP_ERR_INVALID, "unknown act");
+    if ((rc = check_elems("X", M, K)) || (rc = check_elems("W", K, N)) || (rc = check_elems("dY", M, N))) return rc;
+    const bool relu = act == C3HIP_ACT_RELU;
+    if (M > 0 && N > 0 && (!dY || (relu && !Y))) return set_error(C3HIP_ERR_INVALID, "null dY / Y");
+    if (dX && K > 0 && M > 0 && N > 0 && !W) return set_error(C3HIP_ERR_INVALID, "dX needs W");
+    if (dW && K > 0 && N > 0 && M > 0 && !X) return set_error(C3HIP_ERR_INVALID, "dW needs X");
+    const void* mask = relu ? Y : nullptr;
+    if (dX) {
+        // dX[M,K] = dZ[M,N] . W^T : logical (M, N=K, K=N), A = dY (k-contig), B(k=n, j) = W[j*N + n].
+        GemmArgs a{};
+        a.A = dY; a.Amask = mask; a.B = W; a.C = dX;
+        a.M = M; a.N = K; a.K = N;
+        a.lda = N; a.ldb = N; a.ldc = K;
+        rc = run_gemm(dtype, relu ? Kind::DxMask : Kind::Dx, a, true, true, stream);
+        if (rc) return rc;
+    }
+    if (dW) {
+        // dW[K,N] = X^T . dZ : logical (M=K, N, K=M), A(i, m) = X[m*K + i], B(m, j) = dZ[m*N + j].
+        GemmArgs a{};
+        a.A = X; a.B = dY; a.Bmask = mask; a.C = dW; a.db = db;
+        a.M = K; a.N = N; a.K = M;
+        a.lda = K; a.ldb = N; a.ldc = N;
+        if (K == 0 && db) {
+            // No dW rows: no block would visit dY, so the column sums run on their own.
+            a.db = nullptr;
+        } else {
+            rc = run_gemm(dtype, relu ? Kind::DwMask : Kind::Dw, a, false, false, stream);
+            if (rc) return rc;
+            if (N > 0 && a.db) return C3HIP_OK;
+        }
+    }
+    if (db && (!dW || K == 0)) {
+        if (dtype != C3HIP_F32) return set_error(C3HIP_ERR_UNSUPPORTED, "bf16 db without dW");
+        return colsum((const float*)dY, (const float*)mask, db, M, N, stream);
+    }
+    return C3HIP_OK;
+}
+
+int c3hip_sum_reduce(const float* in, float* out, int64_t M, int64_t N, int axis, void* stream_) {
+    clear_error();
+    hipStream_t stream = (hipStream_t)stream_;
+    if (axis != 0 && axis != 1) return set_error(C3HIP_ERR_INVALID, "axis must be 0 or 1");
+    if (M < 0 || N < 0) return set_error(C3HIP_ERR_INVALID, "negative dimension");
+    const int64_t outn = axis == 0 ? N : M;
+    if (outn == 0) return C3HIP_OK;
+    if (!out || (M > 0 && N > 0 && !in)) return set_error(C3HIP_ERR_INVALID, "null pointer");
+    if (axis == 0) return colsum(in, nullptr, out, M, N, stream);
+    void* args[] = {(void*)&in, (void*)&out, &M, &N};
+    return launch("c3_rowsum_f32", dim3((unsigned)((M + 3) / 4)), dim3(256), args, stream);
+}
+
+}  // extern "C"

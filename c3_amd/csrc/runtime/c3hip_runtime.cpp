@@ -1,0 +1,188 @@
+// c3hip_runtime.cpp -- host side of the C ABI in include/c3hip.h.
+//
+// Loads the prebuilt gfx950 code objects (elementwise.hsaco, gemm_f32.hsaco,
+// gemm_bf16.hsaco, reduce.hsaco) with hipModuleLoad, resolves kernels by
+// name, validates arguments, picks the kernel variant (tile shape, vector or
+// scalar loads) and launches it with hipModuleLaunchKernel on the caller's
+// stream.  Device buffers are the caller's; nothing is copied host<->device.
+//
+// The reference's GPU attempt (src/C3/DCUCompiledKernel.cpp:127-209) copied
+// every input host->device and the output back per call and launched one
+// 64-thread block; none of that is repeated here.
+#include "c3hip.h"
+#include "c3hip_internal.h"
+
+#include <dlfcn.h>
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+namespace c3hip {
+
+namespace {
+
+thread_local std::string t_error;
+
+struct DeviceState {
+    int device = -1;
+    std::vector<hipModule_t> modules;
+    std::unordered_map<std::string, hipFunction_t> fns;
+};
+
+std::mutex g_mu;
+std::unordered_map<int, std::unique_ptr<DeviceState>> g_devices;
+
+const char* const kModuleFiles[] = {"elementwise.hsaco", "gemm_f32.hsaco", "reduce.hsaco"};
+
+std::string library_dir() {
+    Dl_info info;
+    if (dladdr((void*)&library_dir, &info) && info.dli_fname) {
+        std::string p(info.dli_fname);
+        const size_t slash = p.rfind('/');
+        if (slash != std::string::npos) return p.substr(0, slash);
+    }
+    return ".";
+}
+
+std::string code_object_dir() {
+    const char* env = std::getenv("C3_HIP_CODE_OBJECT_DIR");
+    if (env && *env) return env;
+    return library_dir();
+}
+
+int load_device(int device, DeviceState** out) {
+    auto it = g_devices.find(device);
+    if (it != g_devices.end()) {
+        *out = it->second.get();
+        return C3HIP_OK;
+    }
+    auto ds = std::make_unique<DeviceState>();
+    ds->device = device;
+    const std::string dir = code_object_dir();
+    for (const char* f : kModuleFiles) {
+        const std::string path = dir + "/" + f;
+        hipModule_t m = nullptr;
+        hipError_t e = hipModuleLoad(&m, path.c_str());
+        if (e != hipSuccess) {
+            for (hipModule_t mm : ds->modules) (void)hipModuleUnload(mm);
+            return set_error(e == hipErrorFileNotFound ? C3HIP_ERR_NOT_FOUND : C3HIP_ERR_HIP,
+                             "hipModuleLoad(" + path + ") failed: " + hipGetErrorString(e));
+        }
+        ds->modules.push_back(m);
+    }
+    *out = ds.get();
+    g_devices.emplace(device, std::move(ds));
+    return C3HIP_OK;
+}
+
+}  // namespace
+
+int set_error(int code, const std::string& msg) {
+    t_error = msg;
+    return code;
+}
+
+void clear_error() { t_error.clear(); }
+
+const char* last_error() { return t_error.c_str(); }
+
+int current_device(int* dev) {
+    hipError_t e = hipGetDevice(dev);
+    if (e != hipSuccess) return set_error(C3HIP_ERR_HIP, std::string("hipGetDevice failed: ") + hipGetErrorString(e));
+    return C3HIP_OK;
+}
+
+int get_function(const char* name, hipFunction_t* fn) {
+    int dev = 0;
+    int rc = current_device(&dev);
+    if (rc) return rc;
+    std::lock_guard<std::mutex> lock(g_mu);
+    DeviceState* ds = nullptr;
+    rc = load_device(dev, &ds);
+    if (rc) return rc;
+    auto it = ds->fns.find(name);
+    if (it != ds->fns.end()) {
+        *fn = it->second;
+        return C3HIP_OK;
+    }
+    for (hipModule_t m : ds->modules) {
+        hipFunction_t f = nullptr;
+        if (hipModuleGetFunction(&f, m, name) == hipSuccess && f) {
+            ds->fns.emplace(name, f);
+            *fn = f;
+            return C3HIP_OK;
+        }
+    }
+    (void)hipGetLastError();  // clear the sticky lookup failures
+    return set_error(C3HIP_ERR_NOT_FOUND, std::string("kernel not found in code objects: ") + name);
+}
+
+int launch(const char* name, dim3 grid, dim3 block, void** args, hipStream_t stream) {
+    hipFunction_t fn = nullptr;
+    int rc = get_function(name, &fn);
+    if (rc) return rc;
+    hipError_t e = hipModuleLaunchKernel(fn, grid.x, grid.y, grid.z, block.x, block.y, block.z, 0, stream, args,
+                                         nullptr);
+    if (e != hipSuccess)
+        return set_error(C3HIP_ERR_HIP, std::string("hipModuleLaunchKernel(") + name + ") failed: " + hipGetErrorString(e));
+    return C3HIP_OK;
+}
+
+int init_device(int device) {
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess) return set_error(C3HIP_ERR_HIP, std::string("hipGetDeviceCount failed: ") + hipGetErrorString(e));
+    if (device < 0 || device >= count)
+        return set_error(C3HIP_ERR_INVALID, "device " + std::to_string(device) + " out of range (count " +
+                                                std::to_string(count) + ")");
+    e = hipSetDevice(device);
+    if (e != hipSuccess) return set_error(C3HIP_ERR_HIP, std::string("hipSetDevice failed: ") + hipGetErrorString(e));
+    std::lock_guard<std::mutex> lock(g_mu);
+    DeviceState* ds = nullptr;
+    return load_device(device, &ds);
+}
+
+int shutdown_all() {
+    std::lock_guard<std::mutex> lock(g_mu);
+    int rc = C3HIP_OK;
+    int prev = -1;
+    (void)hipGetDevice(&prev);
+    for (auto& kv : g_devices) {
+        (void)hipSetDevice(kv.first);
+        for (hipModule_t m : kv.second->modules) {
+            hipError_t e = hipModuleUnload(m);
+            if (e != hipSuccess && rc == C3HIP_OK)
+                rc = set_error(C3HIP_ERR_HIP, std::string("hipModuleUnload failed: ") + hipGetErrorString(e));
+        }
+    }
+    g_devices.clear();
+    if (prev >= 0) (void)hipSetDevice(prev);
+    return rc;
+}
+
+}  // namespace c3hip
+
+extern "C" {
+
+int c3hip_abi_version(void) { return C3HIP_ABI_VERSION; }
+
+const char* c3hip_last_error(void) { return c3hip::last_error(); }
+
+int c3hip_init(int device) {
+    c3hip::clear_error();
+    return c3hip::init_device(device);
+}
+
+int c3hip_shutdown(void) {
+    c3hip::clear_error();
+    return c3hip::shutdown_all();
+}
+
+}  // extern "C"

@@ -1,0 +1,114 @@
+"""ctypes binding of libc3hip.so (the C ABI declared in include/c3hip.h).
+
+This is the binding a Python caller of the backend uses; tests and bench.py
+go through it so every GPU result crosses the same C ABI a C/C++ host would
+call.  Device pointers and streams are plain integers (for example
+``tensor.data_ptr()`` and ``torch.cuda.current_stream().cuda_stream``).
+
+Loading fails loudly when the library is not built: there is no fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+LIB_DIR = Path(__file__).resolve().parent / "lib"
+LIB_PATH = LIB_DIR / "libc3hip.so"
+
+# Status codes, element types, activations and elementwise ops (include/c3hip.h).
+OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP, ERR_NOT_FOUND, ERR_TOO_LARGE = 0, 1, 2, 3, 4, 5
+F32, BF16 = 0, 1
+ACT_NONE, ACT_RELU = 0, 1
+EW_ADD, EW_SUB, EW_MUL, EW_DIV, EW_RELU, EW_RELU_BWD, EW_NEG, EW_SCALE = range(8)
+EW_OPS = {"add": EW_ADD, "sub": EW_SUB, "mul": EW_MUL, "div": EW_DIV, "relu": EW_RELU,
+          "relu_bwd": EW_RELU_BWD, "neg": EW_NEG, "scale": EW_SCALE}
+
+# Every symbol include/c3hip.h declares, with its ctypes signature.
+_vp, _i64, _int, _f = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
+SIGNATURES = {
+    "c3hip_abi_version": (_int, []),
+    "c3hip_last_error": (ctypes.c_char_p, []),
+    "c3hip_init": (_int, [_int]),
+    "c3hip_shutdown": (_int, []),
+    "c3hip_elementwise": (_int, [_int, _int, _vp, _vp, _f, _vp, _i64, _i64, _vp]),
+    "c3hip_matmul": (_int, [_int, _vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _vp]),
+    "c3hip_linear_fwd": (_int, [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _vp]),
+    "c3hip_linear_bwd": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _vp]),
+    "c3hip_sum_reduce": (_int, [_vp, _vp, _i64, _i64, _int, _vp]),
+}
+
+
+class C3HipError(RuntimeError):
+    def __init__(self, fn: str, code: int, msg: str):
+        super().__init__(f"{fn} failed with status {code}: {msg}")
+        self.code = code
+
+
+_lib = None
+
+
+def load(path: str | os.PathLike | None = None) -> ctypes.CDLL:
+    """Load libc3hip.so once and attach the signatures."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = Path(path) if path else LIB_PATH
+    if not p.exists():
+        raise RuntimeError(f"{p} is not built: run `python -m c3_amd.build` (no CPU fallback exists)")
+    # torch wheels carry their own libamdhip64.so.7.  Importing torch first lets
+    # this library bind to that copy (same soname) so device pointers and
+    # streams are shared; otherwise two HIP runtimes would end up in one process.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+    lib = ctypes.CDLL(str(p))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def _check(fn: str, rc: int) -> None:
+    if rc != OK:
+        raise C3HipError(fn, rc, load().c3hip_last_error().decode(errors="replace"))
+
+
+def last_error() -> str:
+    return load().c3hip_last_error().decode(errors="replace")
+
+
+def init(device: int = 0) -> None:
+    _check("c3hip_init", load().c3hip_init(device))
+
+
+def shutdown() -> None:
+    _check("c3hip_shutdown", load().c3hip_shutdown())
+
+
+def elementwise(op: int, dtype: int, a: int, b: int | None, alpha: float, out: int, n: int, bmod: int = 0,
+                stream: int = 0) -> None:
+    _check("c3hip_elementwise", load().c3hip_elementwise(op, dtype, a, b, alpha, out, n, bmod, stream))
+
+
+def matmul(dtype: int, A: int, B: int, C: int, M: int, K: int, N: int, transA: bool = False,
+           transB: bool = False, stream: int = 0) -> None:
+    _check("c3hip_matmul", load().c3hip_matmul(dtype, A, B, C, M, K, N, int(transA), int(transB), stream))
+
+
+def linear_fwd(dtype: int, X: int, W: int, b: int | None, Y: int, M: int, K: int, N: int, act: int = ACT_RELU,
+               stream: int = 0) -> None:
+    _check("c3hip_linear_fwd", load().c3hip_linear_fwd(dtype, X, W, b, Y, M, K, N, act, stream))
+
+
+def linear_bwd(dtype: int, X: int | None, W: int | None, Y: int | None, dY: int, dX: int | None, dW: int | None,
+               db: int | None, M: int, K: int, N: int, act: int = ACT_RELU, stream: int = 0) -> None:
+    _check("c3hip_linear_bwd", load().c3hip_linear_bwd(dtype, X, W, Y, dY, dX, dW, db, M, K, N, act, stream))
+
+
+def sum_reduce(inp: int, out: int, M: int, N: int, axis: int = 0, stream: int = 0) -> None:
+    _check("c3hip_sum_reduce", load().c3hip_sum_reduce(inp, out, M, N, axis, stream))

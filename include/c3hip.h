@@ -1,0 +1,145 @@
+/*
+ * c3hip.h -- C ABI of the MI355X (gfx950) backend for C3's fused
+ * Linear+bias+ReLU hot path and its elementwise ops.
+ *
+ * Plain pointers and sizes only.  Every data pointer is a DEVICE pointer on
+ * the current HIP device; `stream` is a hipStream_t passed as void* (NULL =
+ * the default stream).  Matrices are row-major and contiguous.  Calls are
+ * asynchronous on `stream`; they return 0 on success and a nonzero
+ * C3HIP_ERR_* code otherwise, with a message from c3hip_last_error() (per
+ * thread).  No exception crosses this boundary.
+ *
+ * In the reference the same work is done by JIT-compiled CPU functions that
+ * the registry calls through three raw ABIs (include/C3/C3KernelRegistry.h:61-80):
+ *   C3KernelFunc        (a, b, out, n, M, K, N)              single-node ops
+ *   MultiNodeKernelFunc (inputs[], out, n, M, K, N, scratch) fused regions
+ *   FusedKernelFunc     (inputs[], out, n)                   elementwise chains
+ * Each entry point below names the reference function it replaces.
+ */
+#ifndef C3HIP_H
+#define C3HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define C3HIP_ABI_VERSION 1
+
+/* Status codes. */
+#define C3HIP_OK 0
+#define C3HIP_ERR_INVALID 1      /* bad argument (null pointer, negative size, unknown op/dtype) */
+#define C3HIP_ERR_UNSUPPORTED 2  /* valid request this build does not implement (e.g. bf16 elementwise) */
+#define C3HIP_ERR_HIP 3          /* a HIP runtime call failed */
+#define C3HIP_ERR_NOT_FOUND 4    /* code object or kernel symbol missing */
+#define C3HIP_ERR_TOO_LARGE 5    /* operand beyond the kernels' 32-bit element addressing */
+
+/* Element types. */
+#define C3HIP_F32 0
+#define C3HIP_BF16 1  /* storage bf16 (uint16 bit patterns), fp32 accumulation */
+
+/* Activations (the reference's c3.matmul `act` attribute, include/C3/C3Ops.td:43-87). */
+#define C3HIP_ACT_NONE 0
+#define C3HIP_ACT_RELU 1
+
+/* Elementwise ops. */
+#define C3HIP_EW_ADD 0
+#define C3HIP_EW_SUB 1
+#define C3HIP_EW_MUL 2
+#define C3HIP_EW_DIV 3
+#define C3HIP_EW_RELU 4
+#define C3HIP_EW_RELU_BWD 5 /* out = (a > 0 ? 1 : 0) * b  (a = forward input, b = grad) */
+#define C3HIP_EW_NEG 6
+#define C3HIP_EW_SCALE 7    /* out = a * alpha */
+
+/* ABI version of the loaded library (C3HIP_ABI_VERSION). */
+int c3hip_abi_version(void);
+
+/* Last error message of the calling thread ("" if none). */
+const char* c3hip_last_error(void);
+
+/*
+ * Load the gfx950 code objects for `device` and make it current.  Looks in
+ * $C3_HIP_CODE_OBJECT_DIR, else beside libc3hip.so.  Idempotent; every
+ * compute entry point below also initialises the current device on first
+ * use.  Replaces the JIT step the reference performs per kernel
+ * (mlir::ExecutionEngine::create + lookup("c3_kernel"),
+ * src/C3/MLIRKernelGen.cpp:1676-1682): here the code is prebuilt and only
+ * loaded (hipModuleLoad / hipModuleGetFunction).
+ */
+int c3hip_init(int device);
+
+/* Unload every module and free library-owned device memory (the last step of
+ * shutdownAll, include/C3/C3Cleanup.h:34-40).  Device memory handed out to
+ * callers is not touched. */
+int c3hip_shutdown(void);
+
+/*
+ * Elementwise op over n contiguous elements: out[i] = op(a[li], b[ri]).
+ * bmod > 0: ri = i mod bmod (rhs broadcast, e.g. a bias row); bmod < 0:
+ * li = i mod -bmod (lhs broadcast); 0: no broadcast.  b is ignored (may be
+ * NULL) for relu/neg/scale; alpha is used by scale only.  dtype: C3HIP_F32.
+ * Replaces the single-node C3KernelFunc kernels: BinaryOpLowering /
+ * UnaryOpLowering / ReLUOpLowering (src/C3/C3DialectLowering.cpp:246-350)
+ * dispatched by ConcreteCompiledKernel::execute (src/C3/C3Engine.cpp:457-522),
+ * the LinalgElementwiseKernel ops (src/C3/LinalgElementwiseGen.cpp:142-244),
+ * and the ReLU backward graph Gt+Mul (src/C3/C3BackwardCapture.cpp:501-528).
+ */
+int c3hip_elementwise(int op, int dtype, const void* a, const void* b, float alpha, void* out,
+                      int64_t n, int64_t bmod, void* stream);
+
+/*
+ * C[M,N] = op(A) . op(B), fp32 accumulation.  transA != 0: A is stored
+ * [K,M]; transB != 0: B is stored [N,K]; otherwise A is [M,K], B is [K,N].
+ * fp32 in/out for C3HIP_F32; bf16 A, B and C for C3HIP_BF16.
+ * Replaces the single-node c3.matmul kernel (MatMulOpLowering,
+ * src/C3/C3DialectLowering.cpp:467-610; transA/transB == 112 paths :546-562),
+ * including the MatMul backward kernels dX = grad.B^T and dW = A^T.grad
+ * (buildMatMulBackwardGraph, src/C3/C3BackwardCapture.cpp:681-723).
+ */
+int c3hip_matmul(int dtype, const void* A, const void* B, void* C, int64_t M, int64_t K, int64_t N,
+                 int transA, int transB, void* stream);
+
+/*
+ * Fused Linear forward: Y[M,N] = act(X[M,K] . W[K,N] + b[N]).
+ * b is fp32 (may be NULL: no bias).  C3HIP_F32: X, W, Y fp32.  C3HIP_BF16:
+ * X, W, Y bf16, fp32 accumulation, bias and activation applied in fp32, Y
+ * rounded to nearest-even once.
+ * Replaces the MultiNodeKernelFunc of the MatMul+Add+ReLU region
+ * (inputs [X, W, b], buildMultiNodeMLIR + buildFusedMultiNode,
+ * src/C3/MLIRKernelGen.cpp:610-768, :783-1253; executed by
+ * MultiNodeCompiledKernel::execute, src/C3/C3Engine.cpp:145-235).
+ */
+int c3hip_linear_fwd(int dtype, const void* X, const void* W, const float* b, void* Y, int64_t M,
+                     int64_t K, int64_t N, int act, void* stream);
+
+/*
+ * Fused Linear backward.  With dZ = (Y > 0 ? 1 : 0) * dY when act ==
+ * C3HIP_ACT_RELU (dZ = dY when act == C3HIP_ACT_NONE):
+ *   dX[M,K] = dZ . W^T,  dW[K,N] = X^T . dZ,  db[N] = sum over rows of dZ.
+ * dX, dW and db are each optional (NULL skips it).  dZ is formed inside the
+ * GEMM operand loads and never written.  C3HIP_F32: all fp32.  C3HIP_BF16:
+ * X, W, Y, dY and dX bf16; dW and db fp32.
+ * Replaces the per-node backward kernels the reference installs for one
+ * layer: ReLU (Gt + Mul, src/C3/C3BackwardCapture.cpp:501-528), MatMul in:0
+ * and in:1 (:681-723) and Add in:1 SumReduce (:618-644), looked up through
+ * C3KernelRegistry::tryExecuteBackward (src/C3/C3KernelRegistry.cpp:230-322).
+ */
+int c3hip_linear_bwd(int dtype, const void* X, const void* W, const void* Y, const void* dY, void* dX,
+                     float* dW, float* db, int64_t M, int64_t K, int64_t N, int act, void* stream);
+
+/*
+ * SumReduce of a row-major fp32 [M,N]: axis 0 -> out[N] (column sums),
+ * axis 1 -> out[M] (row sums).  Replaces SumReduceOpLowering
+ * (src/C3/C3DialectLowering.cpp:382-465), the Add backward in:1 kernel
+ * (src/C3/C3BackwardCapture.cpp:618-644).  Uses a library-owned workspace
+ * for axis 0 (grown on demand, freed by c3hip_shutdown).
+ */
+int c3hip_sum_reduce(const float* in, float* out, int64_t M, int64_t N, int axis, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* C3HIP_H */

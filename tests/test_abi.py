@@ -1,0 +1,98 @@
+"""The C-ABI library without a GPU: it loads, exports every symbol declared in
+include/c3hip.h, the code objects hold every kernel the dispatcher can name,
+and argument validation answers before any device work."""
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from c3_amd import native
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "c3hip.h"
+LIB = ROOT / "c3_amd" / "lib"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(c3hip_\w+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    assert declared_symbols() == sorted(native.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    out = subprocess.run(["nm", "-D", "--defined-only", str(native.LIB_PATH)], capture_output=True, text=True,
+                         check=True).stdout
+    exported = set(re.findall(r"\sT\s+(c3hip_\w+)", out))
+    missing = set(declared_symbols()) - exported
+    assert not missing, missing
+    lib = native.load()
+    for name in declared_symbols():
+        assert hasattr(lib, name)
+
+
+def test_abi_version():
+    assert native.load().c3hip_abi_version() == 1
+
+
+def _kernel_symbols(hsaco: Path):
+    readelf = "/opt/rocm/llvm/bin/llvm-readelf"
+    out = subprocess.run([readelf, "--symbols", "--wide", str(hsaco)], capture_output=True, text=True,
+                         check=True).stdout
+    return set(re.findall(r"FUNC\s+GLOBAL\s+\w+\s+\d+\s+(c3_\w+)$", out, flags=re.M))
+
+
+def test_code_objects_hold_every_dispatched_kernel():
+    gemm = _kernel_symbols(LIB / "gemm_f32.hsaco")
+    for kind in ["fwd", "dx", "dx_mask", "dw", "dw_mask", "tt"]:
+        for tile in ["t64x64", "t128x128", "t256x128"]:
+            for v in "vs":
+                assert f"c3_gemm_f32_{kind}_{tile}_{v}" in gemm
+    ew = _kernel_symbols(LIB / "elementwise.hsaco")
+    for op in native.EW_OPS:
+        assert f"c3_ew_{op}_f32_v" in ew and f"c3_ew_{op}_f32_s" in ew
+    red = _kernel_symbols(LIB / "reduce.hsaco")
+    assert {"c3_colsum_partial_f32", "c3_colsum_final_f32", "c3_rowsum_f32"} <= red
+
+
+# Argument validation runs before any HIP call, so it is testable on the CPU.
+def _rc(fn, *args):
+    return getattr(native.load(), fn)(*args)
+
+
+def test_elementwise_validation():
+    assert _rc("c3hip_elementwise", 99, 0, 16, 16, 0.0, 16, 4, 0, None) == native.ERR_INVALID
+    assert "unknown elementwise op" in native.last_error()
+    assert _rc("c3hip_elementwise", 0, 7, 16, 16, 0.0, 16, 4, 0, None) == native.ERR_INVALID
+    assert _rc("c3hip_elementwise", 0, native.BF16, 16, 16, 0.0, 16, 4, 0, None) == native.ERR_UNSUPPORTED
+    assert _rc("c3hip_elementwise", 0, 0, 16, 16, 0.0, 16, -1, 0, None) == native.ERR_INVALID
+    assert _rc("c3hip_elementwise", 0, 0, 16, None, 0.0, 16, 4, 0, None) == native.ERR_INVALID
+    assert _rc("c3hip_elementwise", 0, 0, None, 16, 0.0, 16, 4, 0, None) == native.ERR_INVALID
+    # n == 0 is a successful no-op.
+    assert _rc("c3hip_elementwise", 0, 0, None, None, 0.0, None, 0, 0, None) == native.OK
+    assert native.last_error() == ""
+
+
+def test_gemm_validation():
+    assert _rc("c3hip_matmul", 3, 16, 16, 16, 4, 4, 4, 0, 0, None) == native.ERR_INVALID
+    assert _rc("c3hip_matmul", 0, 16, 16, 16, -1, 4, 4, 0, 0, None) == native.ERR_INVALID
+    assert _rc("c3hip_matmul", 0, 16, 16, None, 4, 4, 4, 0, 0, None) == native.ERR_INVALID
+    assert _rc("c3hip_matmul", 0, 16, 16, 16, 1 << 20, 1 << 13, 4, 0, 0, None) == native.ERR_TOO_LARGE
+    assert _rc("c3hip_matmul", 0, None, None, None, 0, 5, 5, 0, 0, None) == native.OK
+    assert _rc("c3hip_linear_fwd", 0, 16, 16, None, 16, 4, 4, 4, 5, None) == native.ERR_INVALID  # act
+    assert _rc("c3hip_linear_fwd", 0, None, 16, None, 16, 4, 4, 4, 1, None) == native.ERR_INVALID
+    assert _rc("c3hip_linear_bwd", 0, 16, 16, None, 16, 16, None, None, 4, 4, 4, 1, None) == native.ERR_INVALID
+    assert "Y" in native.last_error()
+    assert _rc("c3hip_linear_bwd", 0, None, None, None, 16, 16, None, None, 4, 4, 4, 0, None) == native.ERR_INVALID
+    assert _rc("c3hip_sum_reduce", 16, 16, 4, 4, 2, None) == native.ERR_INVALID
+    assert _rc("c3hip_sum_reduce", None, 16, 4, 0, 0, None) == native.OK
+
+
+def test_python_binding_raises_with_message():
+    with pytest.raises(native.C3HipError) as ei:
+        native.elementwise(42, native.F32, 16, 16, 0.0, 16, 4)
+    assert ei.value.code == native.ERR_INVALID and "unknown elementwise op" in str(ei.value)

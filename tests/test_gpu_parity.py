@@ -1,0 +1,238 @@
+"""GPU parity of the HIP path (through the C ABI) against the oracle.
+
+Integer-valued inputs make every partial sum exact in fp32, so there the GPU
+must match the oracle bit for bit whatever its summation order.  Real-valued
+inputs are checked with the tolerances in tests/parity.py.
+"""
+import numpy as np
+import pytest
+import torch
+
+from c3_amd import native as N
+from oracle import oracle as O
+from tests.parity import (assert_close_gemm, dev, empty, gemm_bound, host, mask_flips, ptr)
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = 1e-5
+
+
+def same_bits(got, ref):
+    """Bit equality, with any NaN payload accepted for a NaN."""
+    got = np.asarray(got, dtype=np.float32)
+    ref = np.asarray(ref, dtype=np.float32)
+    gn, rn = np.isnan(got), np.isnan(ref)
+    assert np.array_equal(gn, rn), f"NaN positions differ ({int((gn != rn).sum())})"
+    g, r = got[~gn].view(np.int32), ref[~rn].view(np.int32)
+    bad = g != r
+    assert not bad.any(), f"{int(bad.sum())} elements differ in bits, first at {np.flatnonzero(bad)[:5]}"
+
+
+def ints(seed, shape, lo=-2, hi=2):
+    return np.random.default_rng(seed).integers(lo, hi + 1, size=shape).astype(np.float32)
+
+
+# ------------------------------------------------------------ elementwise ----
+SPECIALS = np.array([0.0, -0.0, 1.0, -1.0, np.inf, -np.inf, np.nan, 1e-40, -1e-40, 3.4e38, -3.4e38, 1e-30],
+                    dtype=np.float32)
+
+
+@pytest.mark.parametrize("op", list(N.EW_OPS))
+@pytest.mark.parametrize("n", [1 << 16, 1000003, 12])
+def test_elementwise_bit_exact(gpu, stream, op, n):
+    code = N.EW_OPS[op]
+    a = O.normal(100 + code, n)
+    b = O.uniform(200 + code, n, 0.5, 2.0) if op == "div" else O.normal(300 + code, n)
+    a[: len(SPECIALS)] = SPECIALS[: min(n, len(SPECIALS))]
+    b[: len(SPECIALS)] = SPECIALS[::-1][: min(n, len(SPECIALS))]
+    da, db_, out = dev(a), dev(b), empty(n)
+    N.elementwise(code, N.F32, ptr(da), ptr(db_), 0.5, ptr(out), n, 0, stream)
+    with np.errstate(all="ignore"):
+        ref = O.elementwise(code, a, b if code in O.EW_BINARY else None, alpha=0.5)
+    if op == "relu":
+        # relu(-0.0): the reference's maxnum leaves the sign of the zero unspecified.
+        neg0 = (a == 0) & np.signbit(a)
+        got = host(out)
+        assert np.all(got[neg0] == 0)
+        got[neg0] = ref[neg0]
+        same_bits(got, ref)
+    else:
+        same_bits(host(out), ref)
+
+
+@pytest.mark.parametrize("op", ["add", "sub", "mul", "div", "relu_bwd"])
+@pytest.mark.parametrize("bmod", [256, 7, -256, -5])
+def test_elementwise_broadcast(gpu, stream, op, bmod):
+    code = N.EW_OPS[op]
+    n = 256 * 37
+    big = O.normal(400, n)
+    small = O.uniform(401, abs(bmod), 0.5, 2.0)
+    a, b = (big, small) if bmod > 0 else (small, big)
+    out = empty(n)
+    N.elementwise(code, N.F32, ptr(dev(a)), ptr(dev(b)), 0.0, ptr(out), n, bmod, stream)
+    same_bits(host(out), O.elementwise(code, a, b, bmod=bmod))
+
+
+def test_elementwise_unaligned_pointers(gpu, stream):
+    n = 4096
+    a, b = O.normal(500, n + 1), O.normal(501, n + 1)
+    da, db_ = dev(a), dev(b)
+    out = empty(n + 1)
+    N.elementwise(N.EW_ADD, N.F32, ptr(da) + 4, ptr(db_) + 4, 0.0, ptr(out) + 4, n, 0, stream)
+    same_bits(host(out)[1:], a[1:] + b[1:])
+
+
+# ----------------------------------------------------------- fused forward ----
+FWD_SHAPES = [(128, 784, 256), (128, 256, 128), (128, 128, 10), (256, 512, 384), (67, 45, 33), (1, 1, 1),
+              (130, 129, 131), (512, 1024, 1000), (1024, 256, 1024)]
+
+
+@pytest.mark.parametrize("M,K,Nn", FWD_SHAPES)
+@pytest.mark.parametrize("act", [1, 0])
+def test_linear_fwd_integer_bit_exact(gpu, stream, M, K, Nn, act):
+    X, W, b = ints(1, (M, K)), ints(2, (K, Nn)), ints(3, Nn)
+    Y = empty((M, Nn))
+    N.linear_fwd(N.F32, ptr(dev(X)), ptr(dev(W)), ptr(dev(b)), ptr(Y), M, K, Nn, act, stream)
+    same_bits(host(Y), O.linear_fwd(X, W, b, act))
+
+
+@pytest.mark.parametrize("M,K,Nn", FWD_SHAPES)
+def test_linear_fwd_real(gpu, stream, M, K, Nn):
+    X = O.normal(11, (M, K))
+    W = O.normal(12, (K, Nn), 0.0, 1.0 / np.sqrt(K))
+    b = O.normal(13, Nn, 0.0, 0.1)
+    Y = empty((M, Nn))
+    N.linear_fwd(N.F32, ptr(dev(X)), ptr(dev(W)), ptr(dev(b)), ptr(Y), M, K, Nn, 1, stream)
+    got = host(Y)
+    t = O.matmul(X, W)
+    z = O.bias_act(t, b, act=0)
+    ref = O.bias_act(t, b, act=1)
+    bound = gemm_bound(X, W, K)
+    assert_close_gemm(got, ref, bound, FP32_TOL, what="Y")
+    mask_flips(got, z, bound)
+
+
+def test_linear_fwd_no_bias_and_k0(gpu, stream):
+    M, K, Nn = 64, 32, 48
+    X, W = ints(21, (M, K)), ints(22, (K, Nn))
+    Y = empty((M, Nn))
+    N.linear_fwd(N.F32, ptr(dev(X)), ptr(dev(W)), None, ptr(Y), M, K, Nn, 0, stream)
+    same_bits(host(Y), O.matmul(X, W))
+    # K = 0: Y = act(bias).
+    b = O.normal(23, Nn)
+    Y0 = empty((M, Nn))
+    N.linear_fwd(N.F32, None, None, ptr(dev(b)), ptr(Y0), M, 0, Nn, 1, stream)
+    same_bits(host(Y0), np.tile(np.maximum(b, 0), (M, 1)))
+
+
+# ---------------------------------------------------------- fused backward ----
+BWD_SHAPES = [(128, 784, 256), (128, 128, 10), (256, 512, 384), (67, 45, 33), (1, 1, 1), (130, 129, 131),
+              (512, 1000, 1024), (1000, 256, 512)]
+
+
+def _bwd_inputs(seed, M, K, Nn, integer):
+    if integer:
+        X, W, b, dY = ints(seed, (M, K)), ints(seed + 1, (K, Nn)), ints(seed + 2, Nn), ints(seed + 3, (M, Nn))
+    else:
+        X = O.normal(seed, (M, K))
+        W = O.normal(seed + 1, (K, Nn), 0.0, 1.0 / np.sqrt(K))
+        b = O.normal(seed + 2, Nn, 0.0, 0.1)
+        dY = O.normal(seed + 3, (M, Nn))
+    Y = O.linear_fwd(X, W, b, 1)
+    return X, W, Y, dY
+
+
+def _run_bwd(stream, X, W, Y, dY, act, want=("dX", "dW", "db")):
+    M, K = X.shape
+    Nn = W.shape[1]
+    dX = empty((M, K)) if "dX" in want else None
+    dW = empty((K, Nn)) if "dW" in want else None
+    db = empty(Nn) if "db" in want else None
+    keep = [dev(X), dev(W), dev(Y), dev(dY)]
+    N.linear_bwd(N.F32, ptr(keep[0]), ptr(keep[1]), ptr(keep[2]), ptr(keep[3]), ptr(dX), ptr(dW), ptr(db), M, K,
+                 Nn, act, stream)
+    return (None if dX is None else host(dX), None if dW is None else host(dW), None if db is None else host(db))
+
+
+@pytest.mark.parametrize("M,K,Nn", BWD_SHAPES)
+@pytest.mark.parametrize("act", [1, 0])
+def test_linear_bwd_integer_bit_exact(gpu, stream, M, K, Nn, act):
+    X, W, Y, dY = _bwd_inputs(31, M, K, Nn, True)
+    gX, gW, gb = _run_bwd(stream, X, W, Y, dY, act)
+    rX, rW, rb = O.linear_bwd(X, W, Y, dY, act)
+    same_bits(gX, rX)
+    same_bits(gW, rW)
+    same_bits(gb, rb)
+
+
+@pytest.mark.parametrize("M,K,Nn", BWD_SHAPES)
+def test_linear_bwd_real(gpu, stream, M, K, Nn):
+    X, W, Y, dY = _bwd_inputs(41, M, K, Nn, False)
+    gX, gW, gb = _run_bwd(stream, X, W, Y, dY, 1)
+    rX, rW, rb = O.linear_bwd(X, W, Y, dY, 1)
+    dZ = O.relu_mask_mul(Y, dY)
+    assert_close_gemm(gX, rX, gemm_bound(dZ, W.T, Nn), FP32_TOL, what="dX")
+    assert_close_gemm(gW, rW, gemm_bound(X.T, dZ, M), FP32_TOL, what="dW")
+    assert_close_gemm(gb, rb, 2.02 * M * 2.0 ** -24 * np.abs(dZ.astype(np.float64)).sum(0), FP32_TOL, what="db")
+
+
+@pytest.mark.parametrize("want", [("dX",), ("dW",), ("db",), ("dW", "db"), ("dX", "db")])
+def test_linear_bwd_optional_outputs(gpu, stream, want):
+    M, K, Nn = 96, 80, 72
+    X, W, Y, dY = _bwd_inputs(51, M, K, Nn, True)
+    got = _run_bwd(stream, X, W, Y, dY, 1, want)
+    ref = O.linear_bwd(X, W, Y, dY, 1)
+    for g, r, name in zip(got, ref, ("dX", "dW", "db")):
+        if name in want:
+            same_bits(g, r)
+        else:
+            assert g is None
+
+
+def test_linear_bwd_mask_signs_and_nan(gpu, stream):
+    # dZ = mask * dY keeps -0 and propagates NaN/Inf from dY: check through db,
+    # which is the plain column sum of dZ (one row, so no additions change it).
+    M, K, Nn = 1, 4, 8
+    X = np.ones((M, K), dtype=np.float32)
+    W = np.zeros((K, Nn), dtype=np.float32)
+    Y = np.array([[-1, 0, 2, np.nan, -1, -1, 3, 1]], dtype=np.float32)
+    dY = np.array([[-3, -2, 5, 1, np.inf, np.nan, -0.0, 7]], dtype=np.float32)
+    _, _, gb = _run_bwd(stream, X, W, Y, dY, 1, ("db",))
+    _, _, rb = O.linear_bwd(X, W, Y, dY, 1)
+    same_bits(gb, rb)
+    _, _, gb2 = _run_bwd(stream, X, W, Y, dY, 1, ("dW", "db"))
+    same_bits(gb2, rb)
+
+
+# ------------------------------------------------------------- matmul ----
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("M,K,Nn", [(96, 64, 80), (130, 67, 129), (512, 256, 512)])
+def test_matmul_transposes(gpu, stream, ta, tb, M, K, Nn):
+    A = ints(61, (K, M) if ta else (M, K))
+    B = ints(62, (Nn, K) if tb else (K, Nn))
+    C = empty((M, Nn))
+    N.matmul(N.F32, ptr(dev(A)), ptr(dev(B)), ptr(C), M, K, Nn, bool(ta), bool(tb), stream)
+    same_bits(host(C), O.matmul(A, B, transA=bool(ta), transB=bool(tb)))
+    Ar, Br = O.normal(63, A.shape), O.normal(64, B.shape)
+    Cr = empty((M, Nn))
+    N.matmul(N.F32, ptr(dev(Ar)), ptr(dev(Br)), ptr(Cr), M, K, Nn, bool(ta), bool(tb), stream)
+    ref = O.matmul(Ar, Br, transA=bool(ta), transB=bool(tb))
+    bound = gemm_bound(Ar.T if ta else Ar, Br.T if tb else Br, K)
+    assert_close_gemm(host(Cr), ref, bound, FP32_TOL, what="C")
+
+
+# --------------------------------------------------------- sum_reduce ----
+@pytest.mark.parametrize("M,Nn", [(1, 1), (100, 37), (5000, 300), (8192, 4096)])
+@pytest.mark.parametrize("axis", [0, 1])
+def test_sum_reduce(gpu, stream, M, Nn, axis):
+    x = ints(71, (M, Nn), -50, 50)
+    out = empty(Nn if axis == 0 else M)
+    N.sum_reduce(ptr(dev(x)), ptr(out), M, Nn, axis, stream)
+    same_bits(host(out), O.sum_reduce(x, axis))
+    xr = O.normal(72, (M, Nn))
+    outr = empty(Nn if axis == 0 else M)
+    N.sum_reduce(ptr(dev(xr)), ptr(outr), M, Nn, axis, stream)
+    ref = O.sum_reduce(xr, axis)
+    L = M if axis == 0 else Nn
+    bound = 2.02 * L * 2.0 ** -24 * np.abs(xr.astype(np.float64)).sum(axis)
+    assert_close_gemm(host(outr), ref, bound, FP32_TOL, what="sum")

@@ -1,0 +1,281 @@
+"""Pins the oracle (oracle/c3_oracle.c) before it is trusted as the checker.
+
+The reference ships no golden vectors for this path (its tests live in the
+host framework and are not in the repository), so each oracle function is
+pinned by what the mathematics fixes: published known answers, integer
+inputs whose sums are exact in fp32, float64 brute force with the standard
+error bound, and hand-built cases whose result changes if the summation
+order, the FMA contraction, the bias placement or a sign/mask rule changes.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+U = 2.0 ** -24  # unit roundoff of fp32
+
+
+def f32(x):
+    return np.float32(x)
+
+
+# ---------------------------------------------------------------- inputs ----
+def test_splitmix64_published_sequence():
+    # Published SplitMix64 outputs for seed 1234567 (Vigna's splitmix64.c).
+    import ctypes
+
+    lib = O.lib()
+    lib.oracle_splitmix64_next.restype = ctypes.c_uint64
+    lib.oracle_splitmix64_next.argtypes = [ctypes.POINTER(ctypes.c_uint64)]
+    s = ctypes.c_uint64(1234567)
+    got = [lib.oracle_splitmix64_next(ctypes.byref(s)) for _ in range(5)]
+    assert got == [6457827717110365317, 3203168211198807973, 9817491932198370423, 4593380528125082431,
+                   16408922859458223821]
+
+
+def test_fill_distributions():
+    x = O.normal(7, 1 << 16)
+    assert abs(x.mean()) < 0.02 and abs(x.std() - 1.0) < 0.02
+    u = O.uniform(7, 1 << 16, 0.5, 2.0)
+    assert u.min() >= 0.5 and u.max() < 2.0 and abs(u.mean() - 1.25) < 0.01
+    lb = O.labels(3, 10000, 10)
+    assert lb.min() == 0 and lb.max() == 9 and len(np.unique(lb)) == 10
+    # Reproducible from the seed.
+    assert np.array_equal(O.normal(11, 1001), O.normal(11, 1001))
+
+
+# ------------------------------------------------------------------ bf16 ----
+def test_bf16_round_known_answers():
+    one = 1.0
+    cases = {
+        one: one,
+        one + 2.0 ** -8: one,                     # tie -> even (mantissa 0)
+        one + 3 * 2.0 ** -8: one + 2.0 ** -6,     # tie -> even (rounds up)
+        one + 2.0 ** -8 + 2.0 ** -20: one + 2.0 ** -7,  # above the tie
+        -2.5: -2.5,
+        65504.0: 65536.0,
+    }
+    xs = np.array(list(cases), dtype=np.float32)
+    assert np.array_equal(O.round_bf16(xs), np.array(list(cases.values()), dtype=np.float32))
+    r = O.round_bf16(np.array([np.inf, -np.inf, np.nan], dtype=np.float32))
+    assert r[0] == np.inf and r[1] == -np.inf and np.isnan(r[2])
+
+
+def test_bf16_round_is_nearest():
+    x = O.normal(5, 4096, 0.0, 100.0)
+    r = O.round_bf16(x).astype(np.float64)
+    bits = O.pack_bf16(x)
+    assert np.array_equal(O.bf16_bits_to_f32(bits), r.astype(np.float32))
+    # Neighbouring bf16 values (one bf16 ulp away) are never closer.
+    up = O.bf16_bits_to_f32((bits.astype(np.int32) + 1).astype(np.uint16)).astype(np.float64)
+    dn = O.bf16_bits_to_f32((bits.astype(np.int32) - 1).astype(np.uint16)).astype(np.float64)
+    xd = x.astype(np.float64)
+    assert np.all(np.abs(xd - r) <= np.abs(xd - up)) and np.all(np.abs(xd - r) <= np.abs(xd - dn))
+
+
+# -------------------------------------------------------------- maxnum ----
+def test_maxnum_semantics():
+    assert O.maxnum(float("nan"), 0.0) == 0.0
+    assert O.maxnum(0.0, float("nan")) == 0.0
+    assert O.maxnum(-1.5, 0.0) == 0.0
+    assert O.maxnum(2.5, 0.0) == 2.5
+    assert math.copysign(1.0, O.maxnum(-0.0, 0.0)) == 1.0  # relu(-0) = +0 in this restatement
+
+
+# -------------------------------------------------------------- matmul ----
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_matmul_integer_exact(ta, tb):
+    rng = np.random.default_rng(1)
+    M, K, N = 37, 53, 29
+    A = rng.integers(-3, 4, size=(K, M) if ta else (M, K)).astype(np.float32)
+    B = rng.integers(-3, 4, size=(N, K) if tb else (K, N)).astype(np.float32)
+    ref = (A.T if ta else A).astype(np.int64) @ (B.T if tb else B).astype(np.int64)
+    got = O.matmul(A, B, transA=bool(ta), transB=bool(tb))
+    assert np.array_equal(got, ref.astype(np.float32))
+
+
+def test_matmul_float64_error_bound():
+    M, K, N = 24, 300, 19
+    A = O.normal(21, (M, K))
+    B = O.normal(22, (K, N), 0.0, 0.05)
+    got = O.matmul(A, B).astype(np.float64)
+    exact = A.astype(np.float64) @ B.astype(np.float64)
+    bound = 1.01 * K * U * (np.abs(A).astype(np.float64) @ np.abs(B).astype(np.float64))
+    assert np.all(np.abs(got - exact) <= bound)
+
+
+def test_matmul_sequential_k_order():
+    # Sequential sum from 0.0: ((2^24 + 1) + 1) - 2^24 = 0 in fp32 (each +1 is
+    # a tie that rounds back to 2^24).  Pairwise or reordered sums give 1 or 2.
+    A = np.array([[2.0 ** 24, 1.0, 1.0, -(2.0 ** 24)]], dtype=np.float32)
+    B = np.ones((4, 1), dtype=np.float32)
+    assert O.matmul(A, B)[0, 0] == 0.0
+    # Reversed k order gives a different value, so the test sees the order.
+    assert O.matmul(A[:, ::-1], B)[0, 0] == 2.0
+
+
+def test_matmul_no_fma_contraction():
+    # k0 product: -(1 + 2^-11) exactly; k1 product (1 + 2^-12)^2 = 1 + 2^-11 + 2^-24
+    # rounds to 1 + 2^-11 on its own, so the sum is 0.  An FMA would keep 2^-24.
+    a1 = 1.0 + 2.0 ** -12
+    A = np.array([[-(1.0 + 2.0 ** -11), a1]], dtype=np.float32)
+    B = np.array([[1.0], [a1]], dtype=np.float32)
+    assert O.matmul(A, B)[0, 0] == 0.0
+
+
+def test_matmul_tile_does_not_change_bits():
+    A = O.normal(31, (70, 45))
+    B = O.normal(32, (45, 66))
+    assert np.array_equal(O.matmul(A, B, tile=64), O.matmul(A, B, tile=7))
+
+
+# ----------------------------------------------------- fused forward ----
+def test_bias_added_after_accumulation():
+    # Products 1 and 2^24, bias 1.  After: (0+1)+2^24 = 2^24 (tie), +1 = 2^24.
+    # Bias as the accumulator's initial value would give 1+1+2^24 = 2^24 + 2.
+    X = np.array([[1.0, 2.0 ** 24]], dtype=np.float32)
+    W = np.ones((2, 1), dtype=np.float32)
+    b = np.ones(1, dtype=np.float32)
+    assert O.linear_fwd(X, W, b, act=1)[0, 0] == 2.0 ** 24
+
+
+def test_linear_fwd_special_cases():
+    M, K, N = 9, 12, 7
+    W = O.normal(41, (K, N))
+    b = O.normal(42, N)
+    # One-hot rows pick a row of W: Y = relu(W[k] + b).
+    X = np.zeros((M, K), dtype=np.float32)
+    ks = np.arange(M) % K
+    X[np.arange(M), ks] = 1.0
+    Y = O.linear_fwd(X, W, b, act=1)
+    assert np.array_equal(Y, np.maximum(W[ks] + b, 0).astype(np.float32))
+    # W = 0 -> relu(b) in every row; act 0 leaves the bias.
+    Wz = np.zeros((K, N), dtype=np.float32)
+    assert np.array_equal(O.linear_fwd(O.normal(1, (M, K)), Wz, b, 1), np.tile(np.maximum(b, 0), (M, 1)))
+    assert np.array_equal(O.linear_fwd(O.normal(1, (M, K)), Wz, b, 0), np.tile(b, (M, 1)))
+
+
+def test_bias_act_nan_and_broadcast():
+    t = np.array([[np.nan, -1.0, 2.0]], dtype=np.float32)
+    b = np.array([0.0, 0.5, -3.0], dtype=np.float32)
+    y = O.bias_act(t, b, act=1)
+    assert y[0, 0] == 0.0 and y[0, 1] == 0.0 and y[0, 2] == 0.0
+    y0 = O.bias_act(t, b, act=0)
+    assert np.isnan(y0[0, 0]) and y0[0, 1] == -0.5 and y0[0, 2] == -1.0
+
+
+# ---------------------------------------------------------- backward ----
+def test_relu_mask_mul_signs_and_nans():
+    z = np.array([-1.0, -1.0, 2.0, np.nan, -1.0, 0.0, 1e-30], dtype=np.float32)
+    g = np.array([3.0, -3.0, -4.0, 5.0, np.inf, 7.0, 2.0], dtype=np.float32)
+    out = O.relu_mask_mul(z, g)
+    assert out[0] == 0.0 and math.copysign(1, out[0]) == 1
+    assert out[1] == 0.0 and math.copysign(1, out[1]) == -1  # 0 * -3 = -0
+    assert out[2] == -4.0
+    assert out[3] == 0.0                                        # NaN > 0 is false
+    assert np.isnan(out[4])                                     # 0 * inf
+    assert out[5] == 0.0                                        # 0 > 0 is false
+    assert out[6] == 2.0                                        # denormal-free tiny positive
+
+
+def test_sum_reduce_closed_forms():
+    M, N = 513, 37
+    ones = np.ones((M, N), dtype=np.float32)
+    assert np.array_equal(O.sum_reduce(ones, 0), np.full(N, M, dtype=np.float32))
+    assert np.array_equal(O.sum_reduce(ones, 1), np.full(M, N, dtype=np.float32))
+    rng = np.random.default_rng(2)
+    x = rng.integers(-50, 51, size=(M, N)).astype(np.float32)
+    assert np.array_equal(O.sum_reduce(x, 0), x.astype(np.int64).sum(0).astype(np.float32))
+    assert np.array_equal(O.sum_reduce(x, 1), x.astype(np.int64).sum(1).astype(np.float32))
+    # Sequential order (same construction as the matmul order test).
+    col = np.array([[2.0 ** 24], [1.0], [1.0], [-(2.0 ** 24)]], dtype=np.float32)
+    assert O.sum_reduce(col, 0)[0] == 0.0
+
+
+def test_linear_bwd_matches_its_definition():
+    M, K, N = 33, 21, 17
+    X = O.normal(51, (M, K))
+    W = O.normal(52, (K, N), 0.0, 0.3)
+    b = O.normal(53, N, 0.0, 0.1)
+    Y = O.linear_fwd(X, W, b, 1)
+    dY = O.normal(54, (M, N))
+    dX, dW, db = O.linear_bwd(X, W, Y, dY, act=1)
+    mask = (Y > 0).astype(np.float64)
+    dZ = mask * dY
+    # Float64 brute force with the gamma_K bound of the fp32 sequential sums.
+    ex = dZ @ W.astype(np.float64).T
+    assert np.all(np.abs(dX - ex) <= 1.01 * N * U * (np.abs(dZ) @ np.abs(W.astype(np.float64)).T) + 1e-30)
+    ew = X.astype(np.float64).T @ dZ
+    assert np.all(np.abs(dW - ew) <= 1.01 * M * U * (np.abs(X.astype(np.float64)).T @ np.abs(dZ)) + 1e-30)
+    eb = dZ.sum(0)
+    assert np.all(np.abs(db - eb) <= 1.01 * M * U * np.abs(dZ).sum(0) + 1e-30)
+    # act 0: dZ = dY.
+    dX0, dW0, db0 = O.linear_bwd(X, W, Y, dY, act=0)
+    assert np.array_equal(db0, O.sum_reduce(dY, 0))
+    assert np.array_equal(dX0, O.matmul(dY, W, transB=True))
+    # Optional outputs.
+    _, dWo, dbo = O.linear_bwd(X, W, Y, dY, act=1, want=("dW", "db"))
+    assert np.array_equal(dWo, dW) and np.array_equal(dbo, db)
+
+
+def test_linear_bwd_db_all_ones():
+    M, K, N = 40, 3, 5
+    X = np.ones((M, K), dtype=np.float32)
+    W = np.ones((K, N), dtype=np.float32)
+    Y = np.ones((M, N), dtype=np.float32)
+    dY = np.ones((M, N), dtype=np.float32)
+    dX, dW, db = O.linear_bwd(X, W, Y, dY, act=1)
+    assert np.array_equal(db, np.full(N, M, dtype=np.float32))
+    assert np.array_equal(dW, np.full((K, N), M, dtype=np.float32))
+    assert np.array_equal(dX, np.full((M, K), N, dtype=np.float32))
+
+
+# --------------------------------------------------------- elementwise ----
+def test_elementwise_matches_ieee_single_ops():
+    n = 4099
+    a = O.normal(61, n)
+    b = O.normal(62, n)
+    d = O.uniform(63, n, 0.5, 2.0)
+    with np.errstate(all="ignore"):
+        assert np.array_equal(O.elementwise(O.EW_ADD, a, b), a + b)
+        assert np.array_equal(O.elementwise(O.EW_SUB, a, b), a - b)
+        assert np.array_equal(O.elementwise(O.EW_MUL, a, b), a * b)
+        assert np.array_equal(O.elementwise(O.EW_DIV, a, d), a / d)
+        assert np.array_equal(O.elementwise(O.EW_NEG, a), -a)
+        assert np.array_equal(O.elementwise(O.EW_SCALE, a, alpha=0.5), a * np.float32(0.5))
+        assert np.array_equal(O.elementwise(O.EW_RELU, a), np.where(a > 0, a, np.float32(0)))
+        assert np.array_equal(O.elementwise(O.EW_RELU_BWD, a, b), np.where(a > 0, b, np.float32(0) * b))
+
+
+def test_elementwise_special_values_and_broadcast():
+    a = np.array([1.0, -1.0, 0.0, np.nan], dtype=np.float32)
+    z = np.zeros(4, dtype=np.float32)
+    with np.errstate(all="ignore"):
+        r = O.elementwise(O.EW_DIV, a, z)
+    assert r[0] == np.inf and r[1] == -np.inf and np.isnan(r[2]) and np.isnan(r[3])
+    assert O.elementwise(O.EW_RELU, a)[3] == 0.0  # maxnum(NaN, 0) = 0
+    neg = O.elementwise(O.EW_NEG, np.array([0.0], dtype=np.float32))
+    assert math.copysign(1, neg[0]) == -1
+    # bmod > 0 broadcasts the rhs row (bias add), bmod < 0 the lhs.
+    x = O.normal(71, (6, 8))
+    row = O.normal(72, 8)
+    assert np.array_equal(O.elementwise(O.EW_ADD, x, row, bmod=8).reshape(6, 8), x + row)
+    assert np.array_equal(O.elementwise(O.EW_SUB, row, x, bmod=-8).reshape(6, 8), row - x)
+
+
+# -------------------------------------------------------- softmax-CE ----
+def test_softmax_ce_against_float64():
+    M, C = 64, 10
+    logits = O.normal(81, (M, C), 0.0, 3.0)
+    lbl = O.labels(82, M, C)
+    loss, d = O.softmax_ce(logits, lbl)
+    L = logits.astype(np.float64)
+    m = L.max(1, keepdims=True)
+    lse = m[:, 0] + np.log(np.exp(L - m).sum(1))
+    ref = float(np.mean(lse - L[np.arange(M), lbl]))
+    assert abs(loss - ref) <= 1e-5 * max(1.0, abs(ref))
+    p = np.exp(L - lse[:, None])
+    p[np.arange(M), lbl] -= 1.0
+    assert np.max(np.abs(d - p / M)) <= 1e-6
