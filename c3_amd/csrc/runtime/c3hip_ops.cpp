@@ -36,7 +36,7 @@ bool ew_is_binary(int op) {
 
 // ---- GEMM planning -------------------------------------------------------
 
-enum class Kind { Fwd, Dx, DxMask, Dw, DwMask, TT };
+enum class Kind { Fwd, Dx, DxMask, Dw, DwMask, DwB, TT };
 
 const char* kind_name(Kind k) {
     switch (k) {
@@ -45,6 +45,7 @@ const char* kind_name(Kind k) {
         case Kind::DxMask: return "dx_mask";
         case Kind::Dw: return "dw";
         case Kind::DwMask: return "dw_mask";
+        case Kind::DwB: return "dwb";
         case Kind::TT: return "tt";
     }
     return "?";
@@ -56,6 +57,10 @@ struct Tile {
 };
 
 const Tile kF32Tiles[] = {{"t64x64", 64, 64, 256}, {"t128x128", 128, 128, 256}, {"t256x128", 256, 128, 512}};
+const Tile kBf16Tiles[] = {{"t64x64", 64, 64, 256},
+                           {"t128x128", 128, 128, 256},
+                           {"t256x128", 256, 128, 256},
+                           {"t256x256", 256, 256, 256}};
 
 const Tile* find_tile(const Tile* tiles, size_t n, const char* name) {
     for (size_t i = 0; i < n; ++i)
@@ -76,6 +81,24 @@ const Tile* choose_f32_tile(int64_t M, int64_t N) {
     return &kF32Tiles[0];
 }
 
+const Tile* choose_bf16_tile(int64_t M, int64_t N) {
+    const size_t nt = sizeof(kBf16Tiles) / sizeof(kBf16Tiles[0]);
+    if (const char* env = std::getenv("C3_HIP_GEMM_TILE_BF16")) {
+        if (const Tile* t = find_tile(kBf16Tiles, nt, env)) return t;
+    }
+    const int64_t blocks128 = ((M + 127) / 128) * ((N + 127) / 128);
+    if (blocks128 >= 256) return &kBf16Tiles[1];
+    return &kBf16Tiles[0];
+}
+
+// bf16 kernels always move 16-byte vectors (8 elements): the contiguous
+// extent and the leading dimension must be multiples of 8.
+bool bf16_vec_ok(bool kc, int64_t rows, int64_t k, int64_t ld, const void* p, const void* pm) {
+    if (ld % 8 != 0) return false;
+    if (kc ? (k % 8 != 0) : (rows % 8 != 0)) return false;
+    return aligned16(p) && aligned16(pm);
+}
+
 // Can an operand use 16-byte vector loads?  kc: k is its contiguous index.
 bool vec_ok(bool kc, int64_t rows, int64_t k, int64_t ld, const void* p, const void* pm) {
     if (ld % 4 != 0) return false;
@@ -86,7 +109,18 @@ bool vec_ok(bool kc, int64_t rows, int64_t k, int64_t ld, const void* p, const v
 int run_gemm(int dtype, Kind kind, const GemmArgs& a0, bool a_kc, bool b_kc, hipStream_t stream) {
     GemmArgs a = a0;
     if (a.M == 0 || a.N == 0) return C3HIP_OK;
-    if (dtype != C3HIP_F32) return set_error(C3HIP_ERR_UNSUPPORTED, "bf16 GEMM kernels are not built in this library");
+    if (dtype == C3HIP_BF16) {
+        if (!bf16_vec_ok(a_kc, a.M, a.K, a.lda, a.A, a.Amask) || !bf16_vec_ok(b_kc, a.N, a.K, a.ldb, a.B, a.Bmask))
+            return set_error(C3HIP_ERR_UNSUPPORTED,
+                             "bf16 GEMM needs 16-byte aligned operands and contiguous extents that are multiples of 8");
+        const Tile* t = choose_bf16_tile(a.M, a.N);
+        char name[96];
+        std::snprintf(name, sizeof(name), "c3_gemm_bf16_%s_%s", kind_name(kind), t->name);
+        const int64_t blocks = ((a.M + t->bm - 1) / t->bm) * ((a.N + t->bn - 1) / t->bn);
+        if (blocks > 0x7fffffff) return set_error(C3HIP_ERR_TOO_LARGE, "GEMM grid too large");
+        void* args[] = {&a};
+        return launch(name, dim3((unsigned)blocks), dim3(t->threads), args, stream);
+    }
     const Tile* t = choose_f32_tile(a.M, a.N);
     const bool vec = vec_ok(a_kc, a.M, a.K, a.lda, a.A, a.Amask) && vec_ok(b_kc, a.N, a.K, a.ldb, a.B, a.Bmask);
     char name[96];
@@ -196,6 +230,9 @@ int c3hip_matmul(int dtype, const void* A, const void* B, void* C, int64_t M, in
     a.act = C3HIP_ACT_NONE;
     const bool a_kc = !transA, b_kc = transB != 0;
     Kind kind = !transA ? (transB ? Kind::Dx : Kind::Fwd) : (transB ? Kind::TT : Kind::Dw);
+    // bf16 matmul writes bf16 in every case; the dW kind writes fp32 for the
+    // weight gradient, so the plain A^T.B product uses its bf16-output twin.
+    if (dtype == C3HIP_BF16 && kind == Kind::Dw) kind = Kind::DwB;
     return run_gemm(dtype, kind, a, a_kc, b_kc, (hipStream_t)stream);
 }
 

@@ -39,7 +39,7 @@ struct DeviceState {
 std::mutex g_mu;
 std::unordered_map<int, std::unique_ptr<DeviceState>> g_devices;
 
-const char* const kModuleFiles[] = {"elementwise.hsaco", "gemm_f32.hsaco", "reduce.hsaco"};
+const char* const kModuleFiles[] = {"elementwise.hsaco", "gemm_f32.hsaco", "gemm_bf16.hsaco", "reduce.hsaco"};
 
 std::string library_dir() {
     Dl_info info;
@@ -114,13 +114,16 @@ int get_function(const char* name, hipFunction_t* fn) {
     }
     for (hipModule_t m : ds->modules) {
         hipFunction_t f = nullptr;
-        if (hipModuleGetFunction(&f, m, name) == hipSuccess && f) {
+        const hipError_t e = hipModuleGetFunction(&f, m, name);
+        if (e == hipSuccess && f) {
             ds->fns.emplace(name, f);
             *fn = f;
             return C3HIP_OK;
         }
+        // A miss in one module records hipErrorNotFound as the thread's last
+        // HIP error; clear it so it is not reported by an unrelated later call.
+        (void)hipGetLastError();
     }
-    (void)hipGetLastError();  // clear the sticky lookup failures
     return set_error(C3HIP_ERR_NOT_FOUND, std::string("kernel not found in code objects: ") + name);
 }
 

@@ -41,3 +41,20 @@ def stream(gpu):
     import torch
 
     return torch.cuda.current_stream().cuda_stream
+
+
+@pytest.fixture(autouse=True)
+def _release_device_buffers():
+    yield
+    import sys as _sys
+
+    mod = _sys.modules.get("tests.parity")
+    if mod is not None:
+        try:
+            import torch
+
+            if torch.cuda.is_available():
+                torch.cuda.synchronize()
+        except Exception:
+            pass
+        mod.release_buffers()

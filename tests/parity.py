@@ -17,9 +17,24 @@ import torch
 
 U = 2.0 ** -24
 
+# Every buffer made by dev()/dev_bf16()/empty() stays referenced until the
+# test ends (release_buffers(), called by an autouse fixture), so a pointer
+# taken from a temporary, e.g. ptr(dev(x)) inline in a call, stays valid
+# while the asynchronous kernel runs.
+_KEEP: list = []
+
+
+def release_buffers() -> None:
+    _KEEP.clear()
+
+
+def _keep(t: torch.Tensor) -> torch.Tensor:
+    _KEEP.append(t)
+    return t
+
 
 def dev(a: np.ndarray, device="cuda:0") -> torch.Tensor:
-    return torch.from_numpy(np.ascontiguousarray(a)).to(device)
+    return _keep(torch.from_numpy(np.ascontiguousarray(a)).to(device))
 
 
 def dev_bf16(a: np.ndarray, device="cuda:0") -> torch.Tensor:
@@ -27,7 +42,7 @@ def dev_bf16(a: np.ndarray, device="cuda:0") -> torch.Tensor:
     from oracle import oracle as O
 
     bits = O.pack_bf16(a).view(np.int16)
-    return torch.from_numpy(bits.copy()).to(device).view(torch.bfloat16)
+    return _keep(torch.from_numpy(bits.copy()).to(device).view(torch.bfloat16))
 
 
 def host(t: torch.Tensor) -> np.ndarray:
@@ -42,7 +57,7 @@ def empty(shape, dtype=torch.float32, fill=np.nan, device="cuda:0") -> torch.Ten
     """Output buffer pre-filled with NaN so an unwritten element is caught."""
     t = torch.empty(shape, dtype=dtype, device=device)
     t.fill_(float(fill))
-    return t
+    return _keep(t)
 
 
 def ptr(t: torch.Tensor | None):

@@ -236,3 +236,87 @@ def test_sum_reduce(gpu, stream, M, Nn, axis):
     L = M if axis == 0 else Nn
     bound = 2.02 * L * 2.0 ** -24 * np.abs(xr.astype(np.float64)).sum(axis)
     assert_close_gemm(host(outr), ref, bound, FP32_TOL, what="sum")
+
+
+# ------------------------------------------------------------------ bf16 ----
+# bf16 storage, fp32 accumulation.  The oracle runs on the bf16-rounded
+# inputs; Y and dX are rounded once to bf16 (RNE), dW and db stay fp32.
+BF16_TOL = 1e-2
+BF16_SHAPES = [(128, 256, 128), (256, 512, 384), (512, 1024, 1000), (1024, 1024, 1024), (136, 72, 264), (8, 8, 8),
+               (1, 64, 8)]
+
+
+def _bf16_round(x):
+    return O.round_bf16(x)
+
+
+@pytest.mark.parametrize("M,K,Nn", BF16_SHAPES)
+@pytest.mark.parametrize("act", [1, 0])
+def test_bf16_integer_bit_exact(gpu, stream, M, K, Nn, act):
+    from tests.parity import dev_bf16
+
+    X, W, b, dY = ints(81, (M, K)), ints(82, (K, Nn)), ints(83, Nn), ints(84, (M, Nn))
+    Y = empty((M, Nn), dtype=torch.bfloat16)
+    N.linear_fwd(N.BF16, ptr(dev_bf16(X)), ptr(dev_bf16(W)), ptr(dev(b)), ptr(Y), M, K, Nn, act, stream)
+    rY = _bf16_round(O.linear_fwd(X, W, b, act))
+    same_bits(host(Y), rY)
+    dX = empty((M, K), dtype=torch.bfloat16)
+    dW, db = empty((K, Nn)), empty(Nn)
+    N.linear_bwd(N.BF16, ptr(dev_bf16(X)), ptr(dev_bf16(W)), ptr(Y), ptr(dev_bf16(dY)), ptr(dX), ptr(dW), ptr(db),
+                 M, K, Nn, act, stream)
+    rX, rW, rb = O.linear_bwd(X, W, rY, dY, act)
+    same_bits(host(dX), _bf16_round(rX))
+    same_bits(host(dW), rW)
+    same_bits(host(db), rb)
+
+
+@pytest.mark.parametrize("M,K,Nn", BF16_SHAPES)
+def test_bf16_real(gpu, stream, M, K, Nn):
+    from tests.parity import dev_bf16
+
+    X = _bf16_round(O.normal(91, (M, K)))
+    W = _bf16_round(O.normal(92, (K, Nn), 0.0, 1.0 / np.sqrt(K)))
+    b = O.normal(93, Nn, 0.0, 0.1)
+    dY = _bf16_round(O.normal(94, (M, Nn)))
+    Y = empty((M, Nn), dtype=torch.bfloat16)
+    N.linear_fwd(N.BF16, ptr(dev_bf16(X)), ptr(dev_bf16(W)), ptr(dev(b)), ptr(Y), M, K, Nn, 1, stream)
+    t = O.matmul(X, W)
+    z = O.bias_act(t, b, 0)
+    rY = O.bias_act(t, b, 1)
+    gY = host(Y)
+    bound = gemm_bound(X, W, K)
+    assert_close_gemm(gY, rY, bound, BF16_TOL, out_round=2.0 ** -8, what="Y bf16")
+    mask_flips(gY, z, bound + 2.0 ** -8 * np.abs(z))
+    # Backward from the GPU's own Y (its mask is what the backward must use).
+    dX = empty((M, K), dtype=torch.bfloat16)
+    dW, db = empty((K, Nn)), empty(Nn)
+    N.linear_bwd(N.BF16, ptr(dev_bf16(X)), ptr(dev_bf16(W)), ptr(Y), ptr(dev_bf16(dY)), ptr(dX), ptr(dW), ptr(db),
+                 M, K, Nn, 1, stream)
+    rX, rW, rb = O.linear_bwd(X, W, gY, dY, 1)
+    dZ = O.relu_mask_mul(gY, dY)
+    assert_close_gemm(host(dX), rX, gemm_bound(dZ, W.T, Nn), BF16_TOL, out_round=2.0 ** -8, what="dX bf16")
+    assert_close_gemm(host(dW), rW, gemm_bound(X.T, dZ, M), BF16_TOL, what="dW")
+    assert_close_gemm(host(db), rb, 2.02 * M * 2.0 ** -24 * np.abs(dZ.astype(np.float64)).sum(0), BF16_TOL,
+                      what="db")
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_bf16_matmul_transposes(gpu, stream, ta, tb):
+    from tests.parity import dev_bf16
+
+    M, K, Nn = 136, 200, 264
+    A = ints(95, (K, M) if ta else (M, K))
+    B = ints(96, (Nn, K) if tb else (K, Nn))
+    C = empty((M, Nn), dtype=torch.bfloat16)
+    N.matmul(N.BF16, ptr(dev_bf16(A)), ptr(dev_bf16(B)), ptr(C), M, K, Nn, bool(ta), bool(tb), stream)
+    same_bits(host(C), _bf16_round(O.matmul(A, B, transA=bool(ta), transB=bool(tb))))
+
+
+def test_bf16_rejects_unaligned_extents(gpu, stream):
+    from tests.parity import dev_bf16
+
+    X, W = dev_bf16(np.ones((16, 12), np.float32)), dev_bf16(np.ones((12, 16), np.float32))
+    Y = empty((16, 16), dtype=torch.bfloat16)
+    with pytest.raises(N.C3HipError) as ei:
+        N.linear_fwd(N.BF16, ptr(X), ptr(W), None, ptr(Y), 16, 12, 16, 1, stream)
+    assert ei.value.code == N.ERR_UNSUPPORTED
