@@ -168,14 +168,16 @@ def main():
 
 
 def _traffic(kernel: str):
-    """HBM bytes per launch from the committed rocprofv3 PMC summary, if present."""
-    p = ROOT / "profiles" / "traffic.json"
-    if not p.exists():
-        return None
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary
+    (FETCH_SIZE + WRITE_SIZE, scaled by the copy-stream calibration), or None."""
+    p = ROOT / "profiles" / "traffic_fp32_linear_8192x4096x4096.md"
     try:
-        return json.loads(p.read_text()).get(kernel, {}).get("bytes_per_launch")
+        for line in p.read_text().splitlines():
+            if line.startswith("traffic-json:"):
+                return json.loads(line.split(":", 1)[1]).get(kernel, {}).get("bytes_per_launch")
     except (ValueError, OSError):
-        return None
+        pass
+    return None
 
 
 def bench_bf16(torch, C, dev, s, args):
