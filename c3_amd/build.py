@@ -34,6 +34,8 @@ DEVICE_FLAGS = ["--genco", "--no-gpu-bundle-output", f"--offload-arch={ARCH}", "
 
 KERNELS = ["elementwise", "gemm_f32", "gemm_bf16", "reduce"]
 RUNTIME_SOURCES = ["runtime/c3hip_runtime.cpp", "runtime/c3hip_ops.cpp"]
+HOST_SOURCES = sorted(p.name for p in (CSRC / "host" / "src").glob("*.cpp"))
+TESTS_CPP = ROOT / "tests" / "cpp"
 
 
 def _run(cmd: list[str], cwd: Path | None = None) -> None:
@@ -66,6 +68,28 @@ def build_runtime() -> Path:
     return out
 
 
+def build_core() -> Path:
+    """libc3core.so: the C++ dispatch layer (registry, hot-path manager, region
+    registry, JIT cache, engine, backward capture) over libc3hip.so."""
+    out = LIB / "libc3core.so"
+    srcs = [str(CSRC / "host" / "src" / s) for s in HOST_SOURCES]
+    cmd = [HIPCC, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", f"-I{CSRC / 'host' / 'include'}", f"-I{INCLUDE}",
+           *srcs, "-o", str(out), f"-L{LIB}", "-lc3hip", "-Wl,-rpath,$ORIGIN", "-lpthread"]
+    _run(cmd)
+    return out
+
+
+def build_core_tests() -> Path:
+    """tests/cpp/c3core_tests: unit-test runner of the dispatch layer."""
+    out = TESTS_CPP / "c3core_tests"
+    cmd = [HIPCC, "-O1", "-std=c++17", "-Wall", f"-I{CSRC / 'host' / 'include'}", f"-I{INCLUDE}", f"-I{TESTS_CPP}",
+           f"-I{ORACLE}", str(TESTS_CPP / "test_c3core.cpp"), "-o", str(out), f"-L{LIB}", "-lc3core", "-lc3hip",
+           f"-L{ORACLE}", "-loracle", f"-Wl,-rpath,{LIB}", f"-Wl,-rpath,{ORACLE}", "-Wl,-rpath,$ORIGIN/../../c3_amd/lib",
+           "-Wl,-rpath,$ORIGIN/../../oracle", "-lpthread"]
+    _run(cmd)
+    return out
+
+
 def build_oracle() -> Path:
     _run(["make", "-s", "-C", str(ORACLE), "liboracle.so"])
     return ORACLE / "liboracle.so"
@@ -75,7 +99,9 @@ def build_all(verbose: bool = False) -> None:
     built = []
     built += build_code_objects()
     built.append(build_runtime())
+    built.append(build_core())
     built.append(build_oracle())
+    built.append(build_core_tests())
     if verbose:
         for b in built:
             print(f"built {b.relative_to(ROOT)} ({b.stat().st_size} bytes)")

@@ -1,0 +1,203 @@
+// C3Engine.cpp -- see include/C3/C3Engine.h.
+#include "C3/C3Engine.h"
+
+#include <chrono>
+#include <cstdio>
+#include <sstream>
+
+#include "C3/HipCompiledKernel.h"
+#include "C3/JITCache.h"
+#include "C3/RollingHash.h"
+#include "c3hip.h"
+
+namespace ct {
+namespace c3 {
+
+namespace {
+
+const char* kindName(KernelKind k) {
+    switch (k) {
+        case KernelKind::Elementwise: return "elementwise";
+        case KernelKind::MatMul: return "matmul";
+        case KernelKind::LinearFwd: return "linear_fwd";
+        case KernelKind::ReLUBackward: return "relu_bwd";
+        case KernelKind::AddBackwardLhs: return "add_bwd_lhs";
+        case KernelKind::SumReduce: return "sum_reduce";
+        case KernelKind::MatMulBackwardA: return "matmul_bwd_a";
+        case KernelKind::MatMulBackwardB: return "matmul_bwd_b";
+        case KernelKind::LinearBwd: return "linear_bwd";
+    }
+    return "?";
+}
+
+// The default backend: resolve the spec's code object through the JIT cache
+// (cached image if present, else the prebuilt file, which is then cached)
+// and wrap the spec in a HipCompiledKernel.
+std::shared_ptr<CompiledKernel> hipFactory(const KernelSpec& spec, const CompileOptions& opts, std::string* err) {
+    const std::string spec_str = spec.toString();
+    const std::string key = JITCache::makeKey(spec_str, opts.opt_level);
+    const std::string module = spec.moduleName();
+    if (!module.empty() && opts.use_cache && JITCache::isEnabled()) {
+        JITCache& cache = JITCache::getInstance();
+        std::vector<char> image;
+        const std::string hit = cache.lookup(key);
+        if (!hit.empty()) {
+            if (!JITCache::readFile(hit, &image) || image.empty()) {
+                *err = "JITCache: cannot read " + hit;
+                return nullptr;
+            }
+            if (c3hip_load_code_object(module.c_str(), image.data(), image.size()) != C3HIP_OK) {
+                *err = std::string("loading cached code object failed: ") + c3hip_last_error();
+                return nullptr;
+            }
+        } else {
+            char path[4096];
+            if (c3hip_code_object_path(module.c_str(), path, sizeof(path)) != C3HIP_OK ||
+                !JITCache::readFile(path, &image) || image.empty()) {
+                *err = "prebuilt code object for module " + module + " not found";
+                return nullptr;
+            }
+            (void)cache.store(key, image, {"module=" + module, "spec=" + spec_str});
+        }
+    }
+    return std::make_shared<HipCompiledKernel>(spec, opts.opt_level, key);
+}
+
+}  // namespace
+
+std::string KernelSpec::toString() const {
+    std::ostringstream ss;
+    ss << "rh=" << std::hex << RollingHash::hashSequence(op_seq) << std::dec << "|kind=" << kindName(kind)
+       << "|ew=" << ew_op << "|alpha=" << alpha << "|act=" << act << "|t=" << transA << transB << "|axis=" << axis
+       << "|dtype=" << static_cast<int>(dtype) << "|in=";
+    for (const auto& s : input_shapes) ss << shapeToString(s) << ";";
+    ss << "|out=" << shapeToString(out_shape);
+    return ss.str();
+}
+
+std::string KernelSpec::moduleName() const {
+    switch (kind) {
+        case KernelKind::Elementwise:
+        case KernelKind::ReLUBackward: return "elementwise";
+        case KernelKind::SumReduce: return "reduce";
+        case KernelKind::AddBackwardLhs: return "";
+        default: return dtype == DType::kBFloat16 ? "gemm_bf16" : "gemm_f32";
+    }
+}
+
+C3Engine& C3Engine::getInstance() {
+    static C3Engine e;
+    return e;
+}
+
+void C3Engine::setLastError(const std::string& e) {
+    std::lock_guard<std::mutex> lk(mu_);
+    last_error_ = e.size() > 1024 ? e.substr(0, 1024) : e;
+}
+
+std::string C3Engine::getLastCompileError() const {
+    std::lock_guard<std::mutex> lk(mu_);
+    return last_error_;
+}
+
+void C3Engine::setFactoryForTest(Factory f) {
+    std::lock_guard<std::mutex> lk(mu_);
+    factory_ = std::move(f);
+    cache_.clear();
+}
+
+bool C3Engine::hasFactoryForTest() const {
+    std::lock_guard<std::mutex> lk(mu_);
+    return static_cast<bool>(factory_);
+}
+
+std::shared_ptr<CompiledKernel> C3Engine::compile(const KernelSpec& spec, const CompileOptions& opts) {
+    if (shutting_down_.load()) return nullptr;
+    const std::string ckey = std::to_string(opts.opt_level) + "|" + spec.toString();
+    Factory factory;
+    {
+        std::lock_guard<std::mutex> lk(mu_);
+        auto it = cache_.find(ckey);
+        if (it != cache_.end()) {
+            hits_++;
+            return it->second;
+        }
+        factory = factory_;
+    }
+    misses_++;
+    compiles_++;
+    std::shared_ptr<CompiledKernel> k;
+    std::string err;
+    try {
+        k = factory ? factory(spec, opts) : hipFactory(spec, opts, &err);
+    } catch (const std::exception& e) {
+        err = e.what();
+        k = nullptr;
+    }
+    if (!k) {
+        setLastError("[O" + std::to_string(opts.opt_level) + "] " + (err.empty() ? "compile failed" : err));
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lk(mu_);
+    if (cache_.size() >= 256) cache_.erase(cache_.begin());
+    cache_.emplace(ckey, k);
+    return k;
+}
+
+C3Engine::CompileFuture C3Engine::compileAsync(const KernelSpec& spec, const CompileOptions& opts) {
+    auto work = std::async(std::launch::async, [this, spec, opts] { return compile(spec, opts); }).share();
+    const uint32_t tmo = compile_timeout_ms_.load();
+    auto watch = std::async(std::launch::async, [this, work, tmo]() -> std::shared_ptr<CompiledKernel> {
+                     if (work.wait_for(std::chrono::milliseconds(tmo)) != std::future_status::ready) {
+                         timeouts_++;
+                         setLastError("[async-timeout] compile exceeded " + std::to_string(tmo) + " ms");
+                         return nullptr;
+                     }
+                     try {
+                         return work.get();
+                     } catch (...) {
+                         return nullptr;
+                     }
+                 }).share();
+    {
+        std::lock_guard<std::mutex> lk(mu_);
+        workers_.push_back(std::async(std::launch::async, [work, watch] {
+            work.wait();
+            watch.wait();
+        }));
+    }
+    return watch;
+}
+
+C3CacheStats C3Engine::getCacheStats() const {
+    C3CacheStats s;
+    s.hits = hits_.load();
+    s.misses = misses_.load();
+    s.compile_count = compiles_.load();
+    s.async_timeouts = timeouts_.load();
+    std::lock_guard<std::mutex> lk(mu_);
+    s.entries = cache_.size();
+    return s;
+}
+
+void C3Engine::clearCache() {
+    std::lock_guard<std::mutex> lk(mu_);
+    cache_.clear();
+}
+
+void C3Engine::shutdown() {
+    shutting_down_.store(true);
+    std::vector<std::future<void>> ws;
+    {
+        std::lock_guard<std::mutex> lk(mu_);
+        ws.swap(workers_);
+    }
+    for (auto& w : ws)
+        if (w.valid() && w.wait_for(std::chrono::seconds(30)) != std::future_status::ready)
+            c3log(ErrorLevel::WARN, "C3Engine::shutdown: a background compile did not finish in 30 s");
+    clearCache();
+    shutting_down_.store(false);
+}
+
+}  // namespace c3
+}  // namespace ct

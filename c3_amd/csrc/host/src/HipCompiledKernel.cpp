@@ -1,0 +1,179 @@
+// HipCompiledKernel.cpp -- CompiledKernel whose execute() launches the gfx950
+// kernels through the C ABI (include/c3hip.h) on device-resident tensors.
+//
+// Replaces the reference's CPU wrappers ConcreteCompiledKernel::execute
+// (src/C3/C3Engine.cpp:457-522, single ops) and
+// MultiNodeCompiledKernel::execute (:145-235, fused regions): inputs are
+// borrowed, outputs are allocated here (callee-allocated, as in the
+// reference) from the device caching pool, and no host copies are made.
+#include "C3/HipCompiledKernel.h"
+
+#include <stdexcept>
+
+#include "c3hip.h"
+
+namespace ct {
+namespace c3 {
+namespace {
+
+thread_local void* t_stream = nullptr;
+
+int hipDtype(DType t) { return t == DType::kBFloat16 ? C3HIP_BF16 : C3HIP_F32; }
+
+void check(int rc, const char* what) {
+    if (rc != C3HIP_OK) throw std::runtime_error(std::string(what) + ": " + c3hip_last_error());
+}
+
+void requireDevice(const Tensor& t, const char* what) {
+    if (!t.defined()) throw std::runtime_error(std::string(what) + ": undefined tensor");
+    if (t.device() != DeviceType::kHIP) throw std::runtime_error(std::string(what) + ": tensor is not on a HIP device");
+}
+
+}  // namespace
+
+void setCurrentStream(void* stream) { t_stream = stream; }
+void* getCurrentStream() { return t_stream; }
+
+HipCompiledKernel::HipCompiledKernel(KernelSpec spec, int opt_level, std::string cache_key)
+    : spec_(std::move(spec)), key_(std::move(cache_key)) {
+    opt_level_ = opt_level;
+}
+
+std::optional<std::vector<size_t>> HipCompiledKernel::outShape() const {
+    if (spec_.out_shape.empty()) return std::nullopt;
+    return spec_.out_shape;
+}
+
+std::vector<Tensor> HipCompiledKernel::execute(const std::vector<Tensor>& in) {
+    const KernelSpec& s = spec_;
+    auto need = [&](size_t n) {
+        if (in.size() != n)
+            throw std::runtime_error("HipCompiledKernel: expected " + std::to_string(n) + " inputs, got " +
+                                     std::to_string(in.size()));
+        for (size_t i = 0; i < n; ++i) requireDevice(in[i], "HipCompiledKernel input");
+        if (!s.input_shapes.empty()) {
+            for (size_t i = 0; i < n && i < s.input_shapes.size(); ++i)
+                if (!s.input_shapes[i].empty() && in[i].shape() != s.input_shapes[i])
+                    throw std::runtime_error("HipCompiledKernel: input " + std::to_string(i) + " shape " +
+                                             shapeToString(in[i].shape()) + " != compiled " +
+                                             shapeToString(s.input_shapes[i]));
+        }
+    };
+    void* st = t_stream;
+    switch (s.kind) {
+        case KernelKind::Elementwise: {
+            const bool binary = s.ew_op == C3HIP_EW_ADD || s.ew_op == C3HIP_EW_SUB || s.ew_op == C3HIP_EW_MUL ||
+                                s.ew_op == C3HIP_EW_DIV || s.ew_op == C3HIP_EW_RELU_BWD;
+            need(binary ? 2 : 1);
+            const Tensor& a = in[0];
+            if (a.dtype() != DType::kFloat) throw std::runtime_error("elementwise ops take fp32");
+            int64_t bmod = 0;
+            const void* bp = nullptr;
+            if (binary) {
+                const Tensor& b = in[1];
+                if (b.dtype() != DType::kFloat) throw std::runtime_error("elementwise ops take fp32");
+                if (b.numel() != a.numel()) {
+                    if (b.numel() == 0 || a.numel() % b.numel() != 0)
+                        throw std::runtime_error("elementwise: rhs of " + shapeToString(b.shape()) +
+                                                 " does not broadcast to " + shapeToString(a.shape()));
+                    bmod = (int64_t)b.numel();
+                }
+                bp = b.data();
+            }
+            Tensor out(ShapeTag{}, a.shape(), DType::kFloat, DeviceType::kHIP);
+            check(c3hip_elementwise(s.ew_op, C3HIP_F32, a.data(), bp, s.alpha, out.data(), (int64_t)a.numel(), bmod,
+                                    st),
+                  "c3hip_elementwise");
+            return {out};
+        }
+        case KernelKind::MatMul: {
+            need(2);
+            const Tensor &A = in[0], &B = in[1];
+            if (A.shape().size() != 2 || B.shape().size() != 2) throw std::runtime_error("matmul takes 2-D operands");
+            const size_t M = s.transA ? A.shape()[1] : A.shape()[0], K = s.transA ? A.shape()[0] : A.shape()[1];
+            const size_t KB = s.transB ? B.shape()[1] : B.shape()[0], N = s.transB ? B.shape()[0] : B.shape()[1];
+            if (K != KB) throw std::runtime_error("matmul: inner dimensions differ");
+            Tensor C(ShapeTag{}, {M, N}, A.dtype(), DeviceType::kHIP);
+            check(c3hip_matmul(hipDtype(A.dtype()), A.data(), B.data(), C.data(), (int64_t)M, (int64_t)K, (int64_t)N,
+                               s.transA, s.transB, st),
+                  "c3hip_matmul");
+            return {C};
+        }
+        case KernelKind::LinearFwd: {
+            need(3);
+            const Tensor &X = in[0], &W = in[1], &b = in[2];
+            const size_t M = X.shape()[0], K = X.shape()[1], N = W.shape()[1];
+            if (W.shape()[0] != K || b.numel() != N || b.dtype() != DType::kFloat)
+                throw std::runtime_error("linear: shapes of X, W, b do not agree");
+            Tensor Y(ShapeTag{}, {M, N}, X.dtype(), DeviceType::kHIP);
+            check(c3hip_linear_fwd(hipDtype(X.dtype()), X.data(), W.data(), b.data_ptr<float>(), Y.data(), (int64_t)M,
+                                   (int64_t)K, (int64_t)N, s.act, st),
+                  "c3hip_linear_fwd");
+            return {Y};
+        }
+        case KernelKind::ReLUBackward: {
+            need(2);  // [grad, x]
+            const Tensor &g = in[0], &x = in[1];
+            if (g.shape() != x.shape() || g.dtype() != DType::kFloat || x.dtype() != DType::kFloat)
+                throw std::runtime_error("relu backward: grad and input differ in shape or are not fp32");
+            Tensor out(ShapeTag{}, g.shape(), DType::kFloat, DeviceType::kHIP);
+            check(c3hip_elementwise(C3HIP_EW_RELU_BWD, C3HIP_F32, x.data(), g.data(), 0.0f, out.data(),
+                                    (int64_t)g.numel(), 0, st),
+                  "c3hip_elementwise(relu_bwd)");
+            return {out};
+        }
+        case KernelKind::AddBackwardLhs: {
+            need(1);
+            return {in[0]};
+        }
+        case KernelKind::SumReduce: {
+            need(1);
+            const Tensor& g = in[0];
+            if (g.dtype() != DType::kFloat || g.shape().size() != 2) throw std::runtime_error("sum_reduce takes fp32 2-D");
+            const size_t M = g.shape()[0], N = g.shape()[1];
+            Tensor out(ShapeTag{}, {s.axis == 0 ? N : M}, DType::kFloat, DeviceType::kHIP);
+            check(c3hip_sum_reduce(g.data_ptr<float>(), out.data_ptr<float>(), (int64_t)M, (int64_t)N, s.axis, st),
+                  "c3hip_sum_reduce");
+            return {out};
+        }
+        case KernelKind::MatMulBackwardA: {
+            need(2);  // [grad(M,N), B(K,N)] -> grad . B^T (M,K)
+            const Tensor &g = in[0], &B = in[1];
+            const size_t M = g.shape()[0], N = g.shape()[1], K = B.shape()[0];
+            if (B.shape()[1] != N) throw std::runtime_error("matmul backward A: shapes do not agree");
+            Tensor out(ShapeTag{}, {M, K}, g.dtype(), DeviceType::kHIP);
+            check(c3hip_matmul(hipDtype(g.dtype()), g.data(), B.data(), out.data(), (int64_t)M, (int64_t)N, (int64_t)K,
+                               0, 1, st),
+                  "c3hip_matmul(grad.B^T)");
+            return {out};
+        }
+        case KernelKind::MatMulBackwardB: {
+            need(2);  // [grad(M,N), A(M,K)] -> A^T . grad (K,N)
+            const Tensor &g = in[0], &A = in[1];
+            const size_t M = g.shape()[0], N = g.shape()[1], K = A.shape()[1];
+            if (A.shape()[0] != M) throw std::runtime_error("matmul backward B: shapes do not agree");
+            Tensor out(ShapeTag{}, {K, N}, g.dtype(), DeviceType::kHIP);
+            check(c3hip_matmul(hipDtype(g.dtype()), A.data(), g.data(), out.data(), (int64_t)K, (int64_t)M, (int64_t)N,
+                               1, 0, st),
+                  "c3hip_matmul(A^T.grad)");
+            return {out};
+        }
+        case KernelKind::LinearBwd: {
+            need(4);  // [dY, X, W, Y] -> [dX, dW, db]
+            const Tensor &dY = in[0], &X = in[1], &W = in[2], &Y = in[3];
+            const size_t M = X.shape()[0], K = X.shape()[1], N = W.shape()[1];
+            Tensor dX(ShapeTag{}, {M, K}, X.dtype(), DeviceType::kHIP);
+            Tensor dW(ShapeTag{}, {K, N}, DType::kFloat, DeviceType::kHIP);
+            Tensor db(ShapeTag{}, {N}, DType::kFloat, DeviceType::kHIP);
+            check(c3hip_linear_bwd(hipDtype(X.dtype()), X.data(), W.data(), Y.data(), dY.data(), dX.data(),
+                                   dW.data_ptr<float>(), db.data_ptr<float>(), (int64_t)M, (int64_t)K, (int64_t)N,
+                                   s.act, st),
+                  "c3hip_linear_bwd");
+            return {dX, dW, db};
+        }
+    }
+    throw std::runtime_error("HipCompiledKernel: unknown kernel kind");
+}
+
+}  // namespace c3
+}  // namespace ct

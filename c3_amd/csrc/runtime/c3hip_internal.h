@@ -15,6 +15,8 @@ const char* last_error();
 int current_device(int* dev);
 int init_device(int device);
 int shutdown_all();
+int load_code_object(const char* module_name, const void* image, size_t nbytes);
+int code_object_path(const char* module_name, char* buf, size_t buflen);
 
 // Resolve `name` in the current device's code objects (loading them on first use).
 int get_function(const char* name, hipFunction_t* fn);

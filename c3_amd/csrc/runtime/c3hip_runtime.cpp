@@ -33,13 +33,27 @@ thread_local std::string t_error;
 struct DeviceState {
     int device = -1;
     std::vector<hipModule_t> modules;
+    std::vector<std::string> module_names;
     std::unordered_map<std::string, hipFunction_t> fns;
+    bool dir_scanned = false;
 };
 
 std::mutex g_mu;
 std::unordered_map<int, std::unique_ptr<DeviceState>> g_devices;
 
-const char* const kModuleFiles[] = {"elementwise.hsaco", "gemm_f32.hsaco", "gemm_bf16.hsaco", "reduce.hsaco"};
+const char* const kModuleNames[] = {"elementwise", "gemm_f32", "gemm_bf16", "reduce"};
+
+bool known_module(const std::string& name) {
+    for (const char* m : kModuleNames)
+        if (name == m) return true;
+    return false;
+}
+
+bool has_module(const DeviceState& ds, const std::string& name) {
+    for (const auto& n : ds.module_names)
+        if (n == name) return true;
+    return false;
+}
 
 std::string library_dir() {
     Dl_info info;
@@ -57,28 +71,39 @@ std::string code_object_dir() {
     return library_dir();
 }
 
-int load_device(int device, DeviceState** out) {
+DeviceState* device_state(int device) {
     auto it = g_devices.find(device);
-    if (it != g_devices.end()) {
-        *out = it->second.get();
-        return C3HIP_OK;
-    }
+    if (it != g_devices.end()) return it->second.get();
     auto ds = std::make_unique<DeviceState>();
     ds->device = device;
-    const std::string dir = code_object_dir();
-    for (const char* f : kModuleFiles) {
-        const std::string path = dir + "/" + f;
-        hipModule_t m = nullptr;
-        hipError_t e = hipModuleLoad(&m, path.c_str());
-        if (e != hipSuccess) {
-            for (hipModule_t mm : ds->modules) (void)hipModuleUnload(mm);
-            return set_error(e == hipErrorFileNotFound ? C3HIP_ERR_NOT_FOUND : C3HIP_ERR_HIP,
-                             "hipModuleLoad(" + path + ") failed: " + hipGetErrorString(e));
-        }
-        ds->modules.push_back(m);
-    }
-    *out = ds.get();
+    DeviceState* p = ds.get();
     g_devices.emplace(device, std::move(ds));
+    return p;
+}
+
+// Load, on first use per device, every prebuilt module not already
+// registered through c3hip_load_code_object.  The caller holds g_mu and has
+// made `device` current.
+int load_device(int device, DeviceState** out) {
+    DeviceState* ds = device_state(device);
+    if (!ds->dir_scanned) {
+        const std::string dir = code_object_dir();
+        for (const char* name : kModuleNames) {
+            if (has_module(*ds, name)) continue;
+            const std::string path = dir + "/" + name + ".hsaco";
+            hipModule_t m = nullptr;
+            hipError_t e = hipModuleLoad(&m, path.c_str());
+            if (e != hipSuccess) {
+                (void)hipGetLastError();
+                return set_error(e == hipErrorFileNotFound ? C3HIP_ERR_NOT_FOUND : C3HIP_ERR_HIP,
+                                 "hipModuleLoad(" + path + ") failed: " + hipGetErrorString(e));
+            }
+            ds->modules.push_back(m);
+            ds->module_names.push_back(name);
+        }
+        ds->dir_scanned = true;
+    }
+    *out = ds;
     return C3HIP_OK;
 }
 
@@ -152,6 +177,35 @@ int init_device(int device) {
     return load_device(device, &ds);
 }
 
+int load_code_object(const char* module_name, const void* image, size_t nbytes) {
+    if (!module_name || !image || nbytes == 0) return set_error(C3HIP_ERR_INVALID, "null module name or image");
+    if (!known_module(module_name)) return set_error(C3HIP_ERR_INVALID, std::string("unknown module ") + module_name);
+    int dev = 0;
+    int rc = current_device(&dev);
+    if (rc) return rc;
+    std::lock_guard<std::mutex> lock(g_mu);
+    DeviceState* ds = device_state(dev);
+    if (has_module(*ds, module_name)) return C3HIP_OK;
+    hipModule_t m = nullptr;
+    hipError_t e = hipModuleLoadData(&m, image);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return set_error(C3HIP_ERR_HIP, std::string("hipModuleLoadData(") + module_name + ") failed: " +
+                                            hipGetErrorString(e));
+    }
+    ds->modules.push_back(m);
+    ds->module_names.push_back(module_name);
+    return C3HIP_OK;
+}
+
+int code_object_path(const char* module_name, char* buf, size_t buflen) {
+    if (!module_name || !known_module(module_name)) return set_error(C3HIP_ERR_INVALID, "unknown module");
+    const std::string p = code_object_dir() + "/" + module_name + ".hsaco";
+    if (!buf || buflen < p.size() + 1) return set_error(C3HIP_ERR_INVALID, "buffer too small for " + p);
+    std::memcpy(buf, p.c_str(), p.size() + 1);
+    return C3HIP_OK;
+}
+
 int shutdown_all() {
     std::lock_guard<std::mutex> lock(g_mu);
     int rc = C3HIP_OK;
@@ -186,6 +240,16 @@ int c3hip_init(int device) {
 int c3hip_shutdown(void) {
     c3hip::clear_error();
     return c3hip::shutdown_all();
+}
+
+int c3hip_load_code_object(const char* module_name, const void* image, size_t nbytes) {
+    c3hip::clear_error();
+    return c3hip::load_code_object(module_name, image, nbytes);
+}
+
+int c3hip_code_object_path(const char* module_name, char* buf, size_t buflen) {
+    c3hip::clear_error();
+    return c3hip::code_object_path(module_name, buf, buflen);
 }
 
 }  // extern "C"

@@ -31,6 +31,8 @@ SIGNATURES = {
     "c3hip_last_error": (ctypes.c_char_p, []),
     "c3hip_init": (_int, [_int]),
     "c3hip_shutdown": (_int, []),
+    "c3hip_load_code_object": (_int, [ctypes.c_char_p, _vp, ctypes.c_size_t]),
+    "c3hip_code_object_path": (_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_size_t]),
     "c3hip_elementwise": (_int, [_int, _int, _vp, _vp, _f, _vp, _i64, _i64, _vp]),
     "c3hip_matmul": (_int, [_int, _vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _vp]),
     "c3hip_linear_fwd": (_int, [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _vp]),

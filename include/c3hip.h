@@ -77,6 +77,21 @@ int c3hip_init(int device);
 int c3hip_shutdown(void);
 
 /*
+ * Register a code object image for module `module_name` ("elementwise",
+ * "gemm_f32", "gemm_bf16" or "reduce") on the current device, e.g. one read
+ * back from the on-disk JIT cache.  A module already loaded on the device is
+ * kept (returns 0); later lookups use whichever image was loaded first.
+ * Replaces the reference's JITCache read path, which reloads cached LLVM
+ * bitcode into an ExecutionEngine (src/C3/LinalgElementwiseGen.cpp:403-439).
+ */
+int c3hip_load_code_object(const char* module_name, const void* image, size_t nbytes);
+
+/* Write into buf (NUL-terminated, at most buflen bytes) the path of the
+ * prebuilt code object file for `module_name`.  Returns 0, or
+ * C3HIP_ERR_INVALID when buf is too small or the name is unknown. */
+int c3hip_code_object_path(const char* module_name, char* buf, size_t buflen);
+
+/*
  * Elementwise op over n contiguous elements: out[i] = op(a[li], b[ri]).
  * bmod > 0: ri = i mod bmod (rhs broadcast, e.g. a bias row); bmod < 0:
  * li = i mod -bmod (lhs broadcast); 0: no broadcast.  b is ignored (may be

@@ -1,0 +1,638 @@
+// test_c3core.cpp -- unit tests of the C++ dispatch layer (libc3core.so).
+//
+// CPU tests use host tensors and a test kernel factory (no GPU, no HIP
+// calls): they pin the hash / key formulas against their closed forms and
+// check the registry, region registry, cost model, JIT cache, hot-path
+// manager, engine watchdog and backward capture behaviour.  Tests named gpu_*
+// run the same flow on HIP device tensors and are invoked by the GPU pytest.
+#include <unistd.h>
+
+#include <atomic>
+#include <chrono>
+#include <cstdlib>
+#include <cstring>
+#include <fstream>
+#include <thread>
+
+#include "C3/C3BackwardCapture.h"
+#include "C3/C3Cleanup.h"
+#include "C3/C3Config.h"
+#include "C3/C3Engine.h"
+#include "C3/C3HotPathManager.h"
+#include "C3/C3KernelRegistry.h"
+#include "C3/FusionCostModel.h"
+#include "C3/JITCache.h"
+#include "C3/RegionFusion.h"
+#include "C3/RollingHash.h"
+#include "c3hip.h"
+#include "testing.h"
+
+using namespace ct;
+using namespace ct::c3;
+
+namespace {
+
+Tensor host(std::vector<size_t> shape, std::vector<float> v) {
+    Tensor t(ShapeTag{}, shape, DType::kFloat, DeviceType::kCPU);
+    CHECK_EQ(t.numel(), v.size());
+    std::memcpy(t.data(), v.data(), v.size() * 4);
+    return t;
+}
+
+std::vector<float> vals(const Tensor& t) {
+    const float* p = t.data_ptr<float>();
+    return std::vector<float>(p, p + t.numel());
+}
+
+// Host implementation of a KernelSpec, used as the engine's backend in CPU
+// tests.  Also counts how many kernels were built.
+std::atomic<int> g_built{0};
+
+class HostKernel : public CompiledKernel {
+public:
+    HostKernel(KernelSpec s, int opt) : s_(std::move(s)), key_(s_.toString()) { opt_level_ = opt; }
+    const std::string& cacheKey() const override { return key_; }
+    DeviceType targetDevice() const override { return DeviceType::kCPU; }
+    size_t workspaceBytes() const override { return 0; }
+    std::vector<Tensor> execute(const std::vector<Tensor>& in) override {
+        switch (s_.kind) {
+            case KernelKind::Elementwise: {
+                Tensor o(ShapeTag{}, in[0].shape(), DType::kFloat, DeviceType::kCPU);
+                const float* a = in[0].data_ptr<float>();
+                const float* b = in.size() > 1 ? in[1].data_ptr<float>() : nullptr;
+                const size_t bn = in.size() > 1 ? in[1].numel() : 1;
+                float* y = o.data_ptr<float>();
+                for (size_t i = 0; i < o.numel(); ++i) {
+                    const float x = a[i], r = b ? b[i % bn] : 0.f;
+                    switch (s_.ew_op) {
+                        case C3HIP_EW_ADD: y[i] = x + r; break;
+                        case C3HIP_EW_SUB: y[i] = x - r; break;
+                        case C3HIP_EW_MUL: y[i] = x * r; break;
+                        case C3HIP_EW_RELU: y[i] = x > 0 ? x : 0.f; break;
+                        case C3HIP_EW_NEG: y[i] = -x; break;
+                        default: throw std::runtime_error("op");
+                    }
+                }
+                return {o};
+            }
+            case KernelKind::ReLUBackward: {
+                Tensor o(ShapeTag{}, in[0].shape(), DType::kFloat, DeviceType::kCPU);
+                for (size_t i = 0; i < o.numel(); ++i)
+                    o.data_ptr<float>()[i] = (in[1].data_ptr<float>()[i] > 0 ? 1.f : 0.f) * in[0].data_ptr<float>()[i];
+                return {o};
+            }
+            case KernelKind::AddBackwardLhs: return {in[0]};
+            case KernelKind::SumReduce: {
+                const size_t M = in[0].shape()[0], N = in[0].shape()[1];
+                Tensor o(ShapeTag{}, {N}, DType::kFloat, DeviceType::kCPU);
+                for (size_t j = 0; j < N; ++j) {
+                    float s = 0;
+                    for (size_t i = 0; i < M; ++i) s += in[0].data_ptr<float>()[i * N + j];
+                    o.data_ptr<float>()[j] = s;
+                }
+                return {o};
+            }
+            case KernelKind::MatMulBackwardA:
+            case KernelKind::MatMulBackwardB:
+            case KernelKind::MatMul:
+            case KernelKind::LinearFwd: {
+                // C = op(A) op(B) on small host matrices.
+                const bool bwA = s_.kind == KernelKind::MatMulBackwardA, bwB = s_.kind == KernelKind::MatMulBackwardB;
+                const Tensor& A = bwB ? in[1] : in[0];
+                const Tensor& B = bwB ? in[0] : in[1];
+                const bool tA = bwB || (s_.kind == KernelKind::MatMul && s_.transA);
+                const bool tB = bwA || (s_.kind == KernelKind::MatMul && s_.transB);
+                const size_t M = tA ? A.shape()[1] : A.shape()[0], K = tA ? A.shape()[0] : A.shape()[1];
+                const size_t N = tB ? B.shape()[0] : B.shape()[1];
+                Tensor o(ShapeTag{}, {M, N}, DType::kFloat, DeviceType::kCPU);
+                for (size_t i = 0; i < M; ++i)
+                    for (size_t j = 0; j < N; ++j) {
+                        float acc = 0;
+                        for (size_t k = 0; k < K; ++k) {
+                            const float a = tA ? A.data_ptr<float>()[k * M + i] : A.data_ptr<float>()[i * K + k];
+                            const float b = tB ? B.data_ptr<float>()[j * K + k] : B.data_ptr<float>()[k * N + j];
+                            acc += a * b;
+                        }
+                        if (s_.kind == KernelKind::LinearFwd) {
+                            if (in.size() > 2) acc += in[2].data_ptr<float>()[j];
+                            if (s_.act == 1) acc = acc > 0 ? acc : 0.f;
+                        }
+                        o.data_ptr<float>()[i * N + j] = acc;
+                    }
+                return {o};
+            }
+            default: throw std::runtime_error("HostKernel: kind not implemented");
+        }
+    }
+
+private:
+    KernelSpec s_;
+    std::string key_;
+};
+
+struct HostBackend {
+    HostBackend() {
+        C3Engine::getInstance().setFactoryForTest([](const KernelSpec& s, const CompileOptions& o) {
+            g_built++;
+            return std::make_shared<HostKernel>(s, o.opt_level);
+        });
+        reset();
+    }
+    ~HostBackend() {
+        reset();
+        C3Engine::getInstance().setFactoryForTest(nullptr);
+    }
+    static void reset() {
+        C3HotPathManager::instance().waitForPendingCompiles();
+        C3BackwardCapture::getInstance().clear();
+        C3HotPathManager::instance().clear();
+        C3KernelRegistry::getInstance().uninstallAll();
+        RegionFusionRegistry::getInstance().clear();
+        C3Engine::getInstance().clearCache();
+        HotPathConfig cfg;
+        C3HotPathManager::instance().configure(cfg);
+        g_built = 0;
+    }
+};
+
+// A kernel returning a fixed list (or throwing), for registry failure paths.
+class ScriptedKernel : public CompiledKernel {
+public:
+    explicit ScriptedKernel(int opt, std::function<std::vector<Tensor>(const std::vector<Tensor>&)> f)
+        : f_(std::move(f)) {
+        opt_level_ = opt;
+    }
+    const std::string& cacheKey() const override { return key_; }
+    DeviceType targetDevice() const override { return DeviceType::kCPU; }
+    size_t workspaceBytes() const override { return 0; }
+    std::vector<Tensor> execute(const std::vector<Tensor>& in) override { return f_(in); }
+
+private:
+    std::function<std::vector<Tensor>(const std::vector<Tensor>&)> f_;
+    std::string key_ = "scripted";
+};
+
+std::string tmpdir() {
+    char tmpl[] = "/tmp/c3core_test_XXXXXX";
+    const char* d = mkdtemp(tmpl);
+    CHECK(d != nullptr);
+    return d;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ hashes --
+TEST(rolling_hash_closed_forms) {
+    auto p = RollingHash::computePrefixHashes({op::MatMul, op::Add, op::ReLU});
+    CHECK(p == (std::vector<uint64_t>{0, 13, 1705, 223384}));
+    CHECK_EQ(RollingHash::hashSequence({op::MatMul, op::Add, op::Sigmoid}), 223392ull);
+    CHECK_EQ(RollingHash::hashSequence({op::MatMul, op::ReLU}), 1732ull);
+    CHECK_EQ(RollingHash::hashSequence({op::MatMul, op::Sigmoid}), 1740ull);
+    CHECK_EQ(RollingHash::hashSequence({op::Add, op::ReLU}), 291ull);
+    // Sub-range hash equals the hash of the sub-sequence.
+    auto q = RollingHash::computePrefixHashes({op::Neg, op::MatMul, op::Add, op::ReLU, op::Mul});
+    CHECK_EQ(RollingHash::getSubHash(q, 1, 3), 223384ull);
+    CHECK_EQ(RollingHash::getSubHash(q, 0, 0), 5ull);
+    CHECK_EQ(RollingHash::getOpCode(op::CE), 79ull);
+    CHECK_EQ(RollingHash::getOpCode(op::kCount), 101ull);
+}
+
+TEST(rolling_hash_wraps_mod_2_64) {
+    // 40 MatMuls: the polynomial exceeds 2^64; sub-hashes of equal windows agree.
+    std::vector<op> seq(40, op::MatMul);
+    auto p = RollingHash::computePrefixHashes(seq);
+    CHECK_EQ(RollingHash::getSubHash(p, 3, 30), RollingHash::getSubHash(p, 10, 37));
+    CHECK(RollingHash::getSubHash(p, 3, 30) != RollingHash::getSubHash(p, 3, 29));
+}
+
+TEST(region_key_closed_forms) {
+    CHECK_EQ(RegionFusionRegistry::shapeHash({128, 784}), 4784ull);
+    CHECK_EQ(RegionFusionRegistry::shapeHash({128, 256}), 4256ull);
+    CHECK_EQ(RegionFusionRegistry::shapeHash({8192, 4096}), 258080ull);
+    CHECK_EQ(RegionFusionRegistry::regionKey(223384, {128, 784}), 0x12b000036898ull);
+    CHECK_EQ(RegionFusionRegistry::regionKey(223384, {128, 256}), 0x10a000036898ull);
+    CHECK_EQ(RegionFusionRegistry::regionKey(223384, {8192, 4096}), 0x3f02000036898ull);
+}
+
+TEST(registry_fnv_closed_forms) {
+    CHECK_EQ(C3KernelRegistry::hashShapes({128, 784}, {784, 256}), (size_t)0xd3cd56bc81bd4363ull);
+    CHECK_EQ(C3KernelRegistry::hashShapes({1u << 24}, {1u << 24}), (size_t)0x9158189b386f57cbull);
+    KernelShapeInfo s;
+    s.fused_pattern = "MatMul+Add+ReLU";
+    s.lhs_shape = {128, 784};
+    CHECK_EQ(C3KernelRegistry::makeFusedKey(op::ReLU, s), std::string("MatMul+Add+ReLU|9:128:784"));
+}
+
+TEST(cost_model_closed_forms) {
+    const size_t mn = 128 * 256;
+    auto c = FusionCostModel::estimate({op::MatMul, op::Add, op::ReLU}, {mn, mn, mn});
+    CHECK_EQ(c.eager_accesses, 5 * mn);
+    CHECK_EQ(c.saved_accesses, 2 * mn);
+    CHECK(std::fabs(c.gain_ratio - 0.4) < 1e-12);
+    CHECK(c.worthwhile);
+    auto d = FusionCostModel::estimate({op::MatMul, op::ReLU}, {mn, mn});
+    CHECK_EQ(d.saved_accesses, (size_t)0);
+    CHECK(!d.worthwhile);
+    // Elementwise chain Add->ReLU->Neg: eager 5n, saved 4n -> 0.8.
+    auto e = FusionCostModel::estimate({op::Add, op::ReLU, op::Neg}, {10, 10, 10});
+    CHECK(std::fabs(e.gain_ratio - 0.8) < 1e-12);
+    CHECK(FusionCostModel::estimate({}, {}).eager_accesses == 0);
+}
+
+TEST(sha256_fips_vectors) {
+    CHECK_EQ(sha256_hex("abc"), std::string("ba7816bf8f01cfea414140de5dae2223b00361a396177a9cb410ff61f20015ad"));
+    CHECK_EQ(sha256_hex(""), std::string("e3b0c44298fc1c149afbf4c8996fb92427ae41e4649b934ca495991b7852b855"));
+    CHECK_EQ(sha256_hex("abcdbcdecdefdefgefghfghighijhijkijkljklmklmnlmnomnopnopq"),
+             std::string("248d6a61d20638b8e5c026930c3e6039a33ce45964ff2167f6ecedd419db06c1"));
+    CHECK_EQ(sha256_hex(std::string(1000000, 'a')),
+             std::string("cdc76e5c9914fb9281a1c7e284d73e67f1809a48a497200e046d39ccc7112cd0"));
+    // Lengths 55/56/63/64 straddle the padding boundary.
+    CHECK_EQ(sha256_hex(std::string(64, 'a')),
+             std::string("ffe054fe7ae0cb6dc65c3af9b61d5209f439851db43d0ba5997337df154668eb"));
+}
+
+// --------------------------------------------------------------- JITCache --
+TEST(jit_cache_layout_and_versioning) {
+    const std::string dir = tmpdir();
+    setenv("C3_AOT_CACHE_DIR", dir.c_str(), 1);
+    unsetenv("C3_JIT_CACHE_DISABLE");
+    JITCache& c = JITCache::getInstance();
+    CHECK_EQ(c.cacheDir(), dir);
+    const std::string key = JITCache::makeKey("rh=36898|kind=linear_fwd", 3);
+    CHECK_EQ(key, sha256_hex(std::string("c3_jit_") + JITCache::currentJITVersion() + "_3_rh=36898|kind=linear_fwd"));
+    const uint64_t m0 = c.misses(), h0 = c.hits(), s0 = c.stores();
+    CHECK(c.lookup(key).empty());
+    CHECK_EQ(c.misses(), m0 + 1);
+    std::vector<char> img = {'\x7f', 'E', 'L', 'F', 1, 2, 3};
+    const std::string path = c.store(key, img, {"module=gemm_f32"});
+    CHECK_EQ(path, dir + "/c3_jit_" + key + ".hsaco");
+    CHECK_EQ(c.stores(), s0 + 1);
+    CHECK_EQ(c.lookup(key), path);
+    CHECK_EQ(c.hits(), h0 + 1);
+    std::vector<char> back;
+    CHECK(JITCache::readFile(path, &back) && back == img);
+    std::ifstream meta(dir + "/c3_jit_" + key + ".meta");
+    std::string line;
+    std::getline(meta, line);
+    CHECK_EQ(line, std::string(JITCache::currentJITVersion()));
+    // A stale version evicts the entry.
+    { std::ofstream m(dir + "/c3_jit_" + key + ".meta"); m << "jit_v2\n"; }
+    CHECK(c.lookup(key).empty());
+    CHECK(access(path.c_str(), F_OK) != 0);
+    // No temporary files are left behind; evict removes entries.
+    CHECK(!c.store(key, img).empty());
+    c.evict();
+    CHECK(c.lookup(key).empty());
+    setenv("C3_JIT_CACHE_DISABLE", "1", 1);
+    CHECK(!JITCache::isEnabled());
+    unsetenv("C3_JIT_CACHE_DISABLE");
+    CHECK(JITCache::isEnabled());
+    unsetenv("C3_AOT_CACHE_DIR");
+}
+
+// ---------------------------------------------------------------- registry --
+TEST(registry_install_dispatch_and_precedence) {
+    HostBackend hb;
+    auto& R = C3KernelRegistry::getInstance();
+    KernelSpec add;
+    add.kind = KernelKind::Elementwise;
+    add.ew_op = C3HIP_EW_ADD;
+    KernelShapeInfo info;
+    info.lhs_shape = {2, 3};
+    info.rhs_shape = {2, 3};
+    info.out_shape = {2, 3};
+    auto k4 = std::make_shared<HostKernel>(add, 4);
+    R.install(op::Add, DeviceType::kCPU, k4, info);
+    Tensor a = host({2, 3}, {1, 2, 3, 4, 5, 6}), b = host({2, 3}, {10, 20, 30, 40, 50, 60});
+    auto r = R.tryExecute(op::Add, a, b);
+    CHECK(r.has_value());
+    CHECK(vals(*r) == (std::vector<float>{11, 22, 33, 44, 55, 66}));
+    // Other shapes / devices / ops miss.
+    CHECK(!R.tryExecute(op::Add, host({3, 2}, {1, 2, 3, 4, 5, 6}), host({3, 2}, {1, 2, 3, 4, 5, 6})).has_value());
+    CHECK(!R.tryExecute(op::Sub, a, b).has_value());
+    // A lower or equal opt level does not replace; a higher one does.
+    KernelSpec sub = add;
+    sub.ew_op = C3HIP_EW_SUB;
+    const size_t inst0 = R.getStats().install_count;
+    R.install(op::Add, DeviceType::kCPU, std::make_shared<HostKernel>(sub, 2), info);
+    R.install(op::Add, DeviceType::kCPU, std::make_shared<HostKernel>(sub, 4), info);
+    CHECK_EQ(R.getStats().install_count, inst0);
+    CHECK(vals(*R.tryExecute(op::Add, a, b))[0] == 11.f);
+    R.install(op::Add, DeviceType::kCPU, std::make_shared<HostKernel>(sub, 5), info);
+    CHECK(vals(*R.tryExecute(op::Add, a, b))[0] == -9.f);
+    const auto st = R.getStats();
+    CHECK_EQ(st.active_entries, (size_t)1);
+    CHECK(st.hit_count >= 3);
+    R.uninstall(op::Add, DeviceType::kCPU);
+    CHECK(!R.tryExecute(op::Add, a, b).has_value());
+}
+
+TEST(registry_failures_fall_back) {
+    HostBackend hb;
+    auto& R = C3KernelRegistry::getInstance();
+    KernelShapeInfo info;
+    info.lhs_shape = {4};
+    info.out_shape = {4};
+    // A throwing kernel: nullopt and a counted miss, the entry stays.
+    R.install(op::ReLU, DeviceType::kCPU,
+              std::make_shared<ScriptedKernel>(3, [](const std::vector<Tensor>&) -> std::vector<Tensor> {
+                  throw std::runtime_error("boom");
+              }),
+              info);
+    const size_t miss0 = R.getStats().miss_count;
+    CHECK(!R.tryExecuteUnary(op::ReLU, host({4}, {1, -1, 2, -2})).has_value());
+    CHECK_EQ(R.getStats().miss_count, miss0 + 1);
+    CHECK_EQ(R.getStats().active_entries, (size_t)1);
+    // A kernel producing the wrong output shape is uninstalled.
+    R.uninstallAll();
+    R.install(op::Neg, DeviceType::kCPU,
+              std::make_shared<ScriptedKernel>(3, [](const std::vector<Tensor>&) {
+                  return std::vector<Tensor>{host({2}, {0, 0})};
+              }),
+              info);
+    CHECK(!R.tryExecuteUnary(op::Neg, host({4}, {1, 2, 3, 4})).has_value());
+    CHECK_EQ(R.getStats().active_entries, (size_t)0);
+    // An empty result is a miss too.
+    R.install(op::Neg, DeviceType::kCPU,
+              std::make_shared<ScriptedKernel>(3, [](const std::vector<Tensor>&) { return std::vector<Tensor>{}; }),
+              info);
+    CHECK(!R.tryExecuteUnary(op::Neg, host({4}, {1, 2, 3, 4})).has_value());
+    // Fused execution failure returns an undefined tensor.
+    auto bad = std::make_shared<ScriptedKernel>(3, [](const std::vector<Tensor>&) -> std::vector<Tensor> {
+        throw std::runtime_error("bad");
+    });
+    CHECK(!R.executeFusedWithInputs(bad, {host({1}, {1})}, KernelShapeInfo{}).defined());
+}
+
+TEST(registry_backward_entries) {
+    HostBackend hb;
+    auto& R = C3KernelRegistry::getInstance();
+    // Kernel returning its inputs so the feed order is visible.
+    auto echo = std::make_shared<ScriptedKernel>(3, [](const std::vector<Tensor>& in) { return in; });
+    R.installBackward("MatMul|k|in:0", echo, {2, 2}, {2, 3}, {1}, 2);
+    Tensor g = host({2, 2}, {1, 2, 3, 4}), A = host({2, 3}, {0, 0, 0, 0, 0, 0}), B = host({3, 2}, {7, 7, 7, 7, 7, 7});
+    auto r = R.tryExecuteBackward("MatMul|k|in:0", g, {A, B});
+    CHECK(r.has_value() && r->size() == 2);
+    CHECK(vals((*r)[0]) == vals(g));
+    CHECK(vals((*r)[1]) == vals(B));  // fwd_input_map {1} feeds B, not A
+    CHECK(R.hasBackwardKey("MatMul|k|in:0"));
+    CHECK(!R.hasBackwardKey("MatMul|k|in:1"));
+    CHECK(!R.tryExecuteBackward("MatMul|k|in:0", host({4}, {1, 2, 3, 4}), {A, B}).has_value());  // grad shape
+    CHECK(!R.tryExecuteBackward("MatMul|k|in:0", g, {A}).has_value());                          // map out of range
+    R.installBackward("X|in:0", echo, {2, 2}, {2, 2}, {0}, 3);                                  // num_inputs 3
+    CHECK(!R.tryExecuteBackward("X|in:0", g, {A}).has_value());
+}
+
+TEST(registry_fused_entries) {
+    HostBackend hb;
+    auto& R = C3KernelRegistry::getInstance();
+    KernelSpec lin;
+    lin.kind = KernelKind::LinearFwd;
+    lin.act = 1;
+    KernelShapeInfo info;
+    info.lhs_shape = {2, 2};
+    info.rhs_shape = {2, 2};
+    info.out_shape = {2, 2};
+    info.fused_pattern = "MatMul+Add+ReLU";
+    R.installFused(std::make_shared<HostKernel>(lin, 3), op::ReLU, info);
+    CHECK_EQ(R.fusedEntryCount(), (size_t)1);
+    Tensor X = host({2, 2}, {1, 2, 3, 4}), W = host({2, 2}, {1, 0, 0, -1}), b = host({2}, {0.5f, 1});
+    auto y = R.tryExecuteFused(op::ReLU, {X, W, b});
+    CHECK(y.has_value());
+    CHECK(vals(*y) == (std::vector<float>{1.5f, 0, 3.5f, 0}));
+    CHECK(!R.tryExecuteFused(op::Sigmoid, {X, W, b}).has_value());
+    auto f = R.findFusedKernelForSequence({op::MatMul, op::Add, op::ReLU}, DeviceType::kCPU, {2, 2});
+    CHECK(f.has_value() && f->second.fused_pattern == "MatMul+Add+ReLU");
+    CHECK(!R.findFusedKernelForSequence({op::MatMul, op::ReLU}, DeviceType::kCPU).has_value());
+    CHECK(R.findFusedKernelForFirstOp(op::MatMul, {2, 2}, DeviceType::kCPU).has_value());
+    CHECK(R.getStats().fused_hit_count >= 1);
+    R.uninstallFused(op::ReLU, info);
+    CHECK_EQ(R.fusedEntryCount(), (size_t)0);
+}
+
+// ---------------------------------------------------------- region fusion --
+TEST(region_registry_install_and_match) {
+    HostBackend hb;
+    auto& RF = RegionFusionRegistry::getInstance();
+    KernelSpec lin;
+    lin.kind = KernelKind::LinearFwd;
+    auto k = std::make_shared<HostKernel>(lin, 3);
+    const size_t mn = 128 * 256;
+    RF.installWithCost({op::MatMul, op::Add, op::ReLU}, k, {mn, mn, mn}, {{128, 784}, {784, 256}});
+    RF.installWithCost({op::MatMul, op::ReLU}, k, {mn, mn}, {{128, 784}, {784, 256}});
+    CHECK_EQ(RF.entryCount(), (size_t)2);
+    CHECK(RF.mayMatchAsLastOp(op::ReLU));
+    CHECK(!RF.mayMatchAsLastOp(op::Sigmoid));
+    auto e = RF.find(0x12b000036898ull);
+    CHECK(e.has_value() && e->len == 3 && e->cost.worthwhile);
+    CHECK(!RF.find(RegionFusionRegistry::regionKey(1732, {128, 784})).has_value());  // MatMul+ReLU: inactive
+    // Longest match from a position of a dispatch trace.
+    auto p = RollingHash::computePrefixHashes({op::Neg, op::MatMul, op::Add, op::ReLU, op::Mul});
+    auto m = RF.matchFromPosition(p, 1, {128, 784});
+    CHECK(m.has_value() && m->len == 3);
+    CHECK(!RF.matchFromPosition(p, 1, {128, 256}).has_value());  // other first-input shape
+    CHECK(!RF.matchFromPosition(p, 0, {128, 784}).has_value());
+    CHECK(!RF.matchFromPosition(p, 4, {128, 784}).has_value());
+    // Inconsistent out_numels leave the entry inactive.
+    RF.installWithCost({op::MatMul, op::Add, op::ReLU}, k, {mn, mn}, {{64, 64}, {64, 64}});
+    CHECK(!RF.find(RegionFusionRegistry::regionKey(223384, {64, 64})).has_value());
+    RF.clear();
+    CHECK(!RF.mayMatchAsLastOp(op::ReLU));
+}
+
+// ---------------------------------------------------------------- engine ---
+TEST(engine_cache_and_watchdog) {
+    HostBackend hb;
+    auto& E = C3Engine::getInstance();
+    KernelSpec s;
+    s.kind = KernelKind::Elementwise;
+    s.ew_op = C3HIP_EW_NEG;
+    s.input_shapes = {{8}};
+    auto k1 = E.compile(s, {});
+    auto k2 = E.compile(s, {});
+    CHECK(k1 && k1 == k2);
+    CHECK_EQ(g_built.load(), 1);
+    CompileOptions o4;
+    o4.opt_level = 4;
+    CHECK(E.compile(s, o4) != k1);
+    // Watchdog: a backend slower than the timeout yields nullptr + the error.
+    E.setFactoryForTest([](const KernelSpec& sp, const CompileOptions& o) {
+        std::this_thread::sleep_for(std::chrono::milliseconds(300));
+        return std::make_shared<HostKernel>(sp, o.opt_level);
+    });
+    const uint32_t old = E.getCompileTimeoutMs();
+    E.setCompileTimeoutMs(20);
+    const size_t t0 = E.getCacheStats().async_timeouts;
+    auto f = E.compileAsync(s, {});
+    CHECK(f.get() == nullptr);
+    CHECK(E.getLastCompileError().find("[async-timeout]") != std::string::npos);
+    CHECK_EQ(E.getCacheStats().async_timeouts, t0 + 1);
+    E.setCompileTimeoutMs(old);
+    // A failing backend leaves an error and no kernel.
+    E.setFactoryForTest([](const KernelSpec&, const CompileOptions&) -> std::shared_ptr<CompiledKernel> {
+        throw std::runtime_error("no kernel for this spec");
+    });
+    CHECK(E.compile(s, {}) == nullptr);
+    CHECK(E.getLastCompileError().find("no kernel for this spec") != std::string::npos);
+}
+
+// ---------------------------------------------------------------- hot path -
+TEST(hotpath_threshold_dual_tier_install) {
+    HostBackend hb;
+    auto& H = C3HotPathManager::instance();
+    auto& R = C3KernelRegistry::getInstance();
+    for (int i = 0; i < 4; ++i) H.recordCall(op::Add, DeviceType::kCPU, {2, 3}, {2, 3});
+    H.waitForPendingCompiles();
+    CHECK_EQ(H.getStats().compilations_triggered, (size_t)0);
+    H.recordCall(op::Add, DeviceType::kCPU, {2, 3}, {2, 3});
+    H.waitForPendingCompiles();
+    CHECK_EQ(H.getStats().compilations_triggered, (size_t)1);
+    CHECK_EQ(g_built.load(), 2);  // O2 and O4 tiers
+    auto r = R.tryExecute(op::Add, host({2, 3}, {1, 1, 1, 1, 1, 1}), host({2, 3}, {1, 2, 3, 4, 5, 6}));
+    CHECK(r.has_value() && vals(*r)[5] == 7.f);
+    // Within the cooldown further hot calls do not recompile.
+    for (int i = 0; i < 10; ++i) H.recordCall(op::Add, DeviceType::kCPU, {2, 3}, {2, 3});
+    H.waitForPendingCompiles();
+    CHECK_EQ(H.getStats().compilations_triggered, (size_t)1);
+    CHECK(H.getStats().cooldown_hits >= 1);
+    // MPS calls are ignored; unsupported ops trigger but build nothing.
+    H.recordCall(op::Add, DeviceType::kMPS, {9}, {9});
+    for (int i = 0; i < 5; ++i) H.recordCall(op::Tanh, DeviceType::kCPU, {4});
+    H.waitForPendingCompiles();
+    CHECK_EQ(g_built.load(), 2);
+}
+
+TEST(hotpath_backpressure) {
+    HostBackend hb;
+    auto& H = C3HotPathManager::instance();
+    HotPathConfig cfg;
+    cfg.max_pending = 0;
+    H.configure(cfg);
+    for (int i = 0; i < 6; ++i) H.recordCall(op::Mul, DeviceType::kCPU, {4}, {4});
+    CHECK(H.getStats().backpressure_hits >= 6);
+    CHECK_EQ(H.getStats().compilations_triggered, (size_t)0);
+}
+
+TEST(hotpath_fused_pattern_installs_region) {
+    HostBackend hb;
+    auto& H = C3HotPathManager::instance();
+    // Autograd-scope calls: MatMul [3,4]x[4,2], Add [3,2]+[2], ReLU [3,2].
+    H.recordCall(op::MatMul, DeviceType::kCPU, {3, 4}, {4, 2}, true);
+    H.recordCall(op::Add, DeviceType::kCPU, {3, 2}, {2}, true);
+    H.recordCall(op::ReLU, DeviceType::kCPU, {3, 2}, {}, true);
+    H.waitForPendingCompiles();
+    CHECK_EQ(C3KernelRegistry::getInstance().fusedEntryCount(), (size_t)1);
+    auto e = RegionFusionRegistry::getInstance().find(RegionFusionRegistry::regionKey(223384, {3, 4}));
+    CHECK(e.has_value() && e->cost.worthwhile);
+    // The region kernel computes relu(X W + b).
+    Tensor X = host({3, 4}, {1, 0, 0, 0, 0, 1, 0, 0, 0, 0, 1, 1});
+    Tensor W = host({4, 2}, {1, -1, 2, -2, 3, -3, 4, -4});
+    Tensor b = host({2}, {0.5f, 0.5f});
+    Tensor y = C3KernelRegistry::getInstance().executeFusedWithInputs(e->kernel, {X, W, b}, KernelShapeInfo{});
+    CHECK(vals(y) == (std::vector<float>{1.5f, 0, 2.5f, 0, 7.5f, 0}));
+    // Repeated detections (every training step) do not rebuild.
+    const int built = g_built.load();
+    for (int i = 0; i < 3; ++i) {
+        H.recordCall(op::MatMul, DeviceType::kCPU, {3, 4}, {4, 2}, true);
+        H.recordCall(op::Add, DeviceType::kCPU, {3, 2}, {2}, true);
+        H.recordCall(op::ReLU, DeviceType::kCPU, {3, 2}, {}, true);
+    }
+    H.waitForPendingCompiles();
+    CHECK_EQ(g_built.load(), built);
+    // Sigmoid epilogue: detected, no kernel.
+    H.recordCall(op::MatMul, DeviceType::kCPU, {5, 4}, {4, 2}, true);
+    H.recordCall(op::Add, DeviceType::kCPU, {5, 2}, {2}, true);
+    H.recordCall(op::Sigmoid, DeviceType::kCPU, {5, 2}, {}, true);
+    H.waitForPendingCompiles();
+    CHECK(H.getStats().patterns_unsupported >= 1);
+    CHECK_EQ(g_built.load(), built);
+}
+
+TEST(hotpath_spec_builders) {
+    KernelSpec s;
+    CHECK(C3HotPathManager::buildSingleOpSpec(op::Div, {7}, {7}, DType::kFloat, &s));
+    CHECK(s.kind == KernelKind::Elementwise && s.ew_op == C3HIP_EW_DIV && s.input_shapes.size() == 2);
+    CHECK(C3HotPathManager::buildSingleOpSpec(op::MatMul, {8, 4}, {4, 2}, DType::kBFloat16, &s));
+    CHECK(s.kind == KernelKind::MatMul && s.out_shape == (std::vector<size_t>{8, 2}) && s.moduleName() == "gemm_bf16");
+    CHECK(!C3HotPathManager::buildSingleOpSpec(op::MatMul, {8, 4}, {3, 2}, DType::kFloat, &s));
+    CHECK(!C3HotPathManager::buildSingleOpSpec(op::Sigmoid, {8}, {}, DType::kFloat, &s));
+    using R = C3HotPathManager::DispatchRecord;
+    std::vector<R> recs = {R{op::MatMul, {8, 4, 4, 2}, {8, 4}, {4, 2}, DType::kFloat, {}},
+                           R{op::Add, {8, 2, 2}, {8, 2}, {2}, DType::kFloat, {}},
+                           R{op::ReLU, {8, 2}, {8, 2}, {}, DType::kFloat, {}}};
+    CHECK(C3HotPathManager::buildFusedSpec(recs, "MatMul+Add+ReLU", &s));
+    CHECK(s.kind == KernelKind::LinearFwd && s.act == 1 && s.input_shapes[2] == (std::vector<size_t>{2}));
+    CHECK(s.op_seq == (std::vector<op>{op::MatMul, op::Add, op::ReLU}) && s.moduleName() == "gemm_f32");
+    recs[1].rhs_shape = {8, 2};  // not a bias row: no fused kernel
+    CHECK(!C3HotPathManager::buildFusedSpec(recs, "MatMul+Add+ReLU", &s));
+    CHECK(!C3HotPathManager::buildFusedSpec(recs, "MatMul+Add+Sigmoid", &s));
+}
+
+// -------------------------------------------------------- backward capture -
+TEST(backward_capture_rules_and_keys) {
+    HostBackend hb;
+    auto& B = C3BackwardCapture::getInstance();
+    Tensor g = host({2, 2}, {1, -2, 3, -4});
+    Tensor x = host({2, 2}, {-1, 0, 2, 5});
+    CHECK_EQ(C3BackwardCapture::makeBaseKey("ReLU", g, {x}), std::string("ReLU|grad:2,2,|inputs:2,2,"));
+    CHECK(!B.tryExecuteBackward("ReLU", g, {x}).has_value());  // miss: compiles in the background
+    B.waitForPendingCompiles();
+    auto r = B.tryExecuteBackward("ReLU", g, {x});
+    CHECK(r.has_value() && vals((*r)[0]) == (std::vector<float>{0, -0.f, 3, -4}));
+    // Add with a bias row: in:0 identity, in:1 column sums.
+    Tensor t = host({2, 2}, {0, 0, 0, 0}), bias = host({2}, {0, 0});
+    CHECK(!B.tryExecuteBackward("Add", g, {t, bias}).has_value());
+    B.waitForPendingCompiles();
+    auto ra = B.tryExecuteBackward("Add", g, {t, bias});
+    CHECK(ra.has_value() && ra->size() == 2);
+    CHECK(vals((*ra)[0]) == vals(g));
+    CHECK(vals((*ra)[1]) == (std::vector<float>{4, -6}));
+    // MatMul: dA = g B^T, dB = A^T g.
+    Tensor A = host({2, 3}, {1, 0, 2, 0, 1, 0}), Bm = host({3, 2}, {1, 2, 3, 4, 5, 6});
+    CHECK(!B.tryExecuteBackward("MatMul", g, {A, Bm}).has_value());
+    B.waitForPendingCompiles();
+    auto rm = B.tryExecuteBackward("MatMul", g, {A, Bm});
+    CHECK(rm.has_value() && rm->size() == 2);
+    CHECK(vals((*rm)[0]) == (std::vector<float>{-3, -5, -7, -5, -7, -9}));
+    CHECK(vals((*rm)[1]) == (std::vector<float>{1, -2, 3, -4, 2, -4}));
+    // Unknown node types are refused; a key compiles once even on repeated misses.
+    CHECK(!B.tryExecuteBackward("Softmax", g, {x}).has_value());
+    const auto st = B.getStats();
+    CHECK(st.cache_hit_count == 3 && st.cache_miss_count == 3 && st.compiles_submitted == 5);
+}
+
+TEST(config_kill_switches) {
+    HostBackend hb;
+    setenv("C3_DISABLE_BACKWARD", "1", 1);
+    reloadConfig();
+    CHECK(!backwardFusionEnabled());
+    Tensor g = host({2}, {1, 2});
+    CHECK(!C3BackwardCapture::getInstance().tryExecuteBackward("ReLU", g, {g}).has_value());
+    CHECK_EQ(C3BackwardCapture::getInstance().getStats().compiles_submitted, (size_t)0);
+    unsetenv("C3_DISABLE_BACKWARD");
+    setenv("C3_DISABLE_HOTPATH", "1", 1);
+    reloadConfig();
+    const size_t c0 = C3HotPathManager::instance().getStats().calls_tracked;
+    C3HotPathManager::instance().recordCall(op::Add, DeviceType::kCPU, {2}, {2});
+    CHECK_EQ(C3HotPathManager::instance().getStats().calls_tracked, c0);
+    unsetenv("C3_DISABLE_HOTPATH");
+    reloadConfig();
+    CHECK(backwardFusionEnabled() && hotPathTrackingEnabled() && regionFusionEnabled() && singleKernelEnabled());
+}
+
+TEST(shutdown_all_clears_state) {
+    HostBackend hb;
+    auto& H = C3HotPathManager::instance();
+    for (int i = 0; i < 5; ++i) H.recordCall(op::Neg, DeviceType::kCPU, {3});
+    shutdownAll();
+    CHECK_EQ(C3KernelRegistry::getInstance().getStats().active_entries, (size_t)0);
+    CHECK_EQ(RegionFusionRegistry::getInstance().entryCount(), (size_t)0);
+    CHECK_EQ(C3Engine::getInstance().getCacheStats().entries, (size_t)0);
+    // The manager accepts work again after shutdown.
+    H.recordCall(op::Neg, DeviceType::kCPU, {3});
+    CHECK(H.getStats().calls_tracked >= 1);
+}
+
+#include "test_c3core_gpu.inc"
+
+int main(int argc, char** argv) { return run_tests(argc, argv); }
