@@ -27,28 +27,6 @@ namespace {
 constexpr int kBK = 64;       // k depth of one LDS stage
 constexpr int kStride = 72;   // bf16 elements per LDS row (64 + 8 padding)
 
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-
-// bf16 bits: Y > 0 <=> sign clear, nonzero, not NaN (+inf counts as > 0).
-__device__ __forceinline__ bool bf16_gt0(unsigned short y) { return (short)y > 0 && y <= 0x7f80u; }
-
-// (Y > 0 ? 1 : 0) * dY on bf16 bit patterns: dY when Y > 0, else a zero with
-// dY's sign, or NaN when dY is Inf/NaN (0 * Inf = NaN).
-__device__ __forceinline__ unsigned short bf16_mask_mul(unsigned short y, unsigned short d) {
-    if (bf16_gt0(y)) return d;
-    if ((d & 0x7f80u) == 0x7f80u) return 0x7fc0u;
-    return d & 0x8000u;
-}
-
-__device__ __forceinline__ uint32_t mask_mul2(uint32_t y, uint32_t d) {
-    return (uint32_t)bf16_mask_mul((unsigned short)(y & 0xffff), (unsigned short)(d & 0xffff)) |
-           ((uint32_t)bf16_mask_mul((unsigned short)(y >> 16), (unsigned short)(d >> 16)) << 16);
-}
-
-__device__ __forceinline__ u32x4 mask_mul8(u32x4 y, u32x4 d) {
-    return u32x4{mask_mul2(y[0], d[0]), mask_mul2(y[1], d[1]), mask_mul2(y[2], d[2]), mask_mul2(y[3], d[3])};
-}
-
 // Global -> register -> LDS staging of one ROWS x 64 operand tile.
 template <int ROWS, int NT, bool KC, bool MASK>
 struct Bf16Loader {
@@ -296,3 +274,206 @@ C3_GEMM_BF16_KINDS(t64x64, 64, 64, 2, 2)
 C3_GEMM_BF16_KINDS(t128x128, 128, 128, 2, 2)
 C3_GEMM_BF16_KINDS(t256x128, 256, 128, 2, 2)
 C3_GEMM_BF16_KINDS(t256x256, 256, 256, 2, 2)
+
+// ===========================================================================
+// Direct-to-LDS variant (suffix _d): 256-thread blocks of 2x2 waves, each
+// wave a 128x128 sub-tile (16 MFMA blocks), 64-deep k tiles, double-buffered.
+// Global tiles go straight into LDS with global_load_lds_dwordx4 (lane l's
+// 16 bytes land at base + 16*l of the instruction's 1 KiB), so no staging
+// registers and no LDS stores are needed.  Layouts, per operand:
+//   KC (k contiguous in global): LDS [row][64 k], 128 B per row; the 16-byte
+//     chunk holding k 8c..8c+7 of row r sits in slot c ^ (r % 8), so the
+//     fragment reads of 8 consecutive rows hit 8 different bank groups.
+//     Fragment: one ds_read_b128 (8 consecutive k of one row).
+//   RC (row contiguous in global): LDS [64 k][ROWS], the chunk holding rows
+//     8c..8c+7 of k-row kr sits in slot c ^ (2 * (kr % 4)).  Fragment: two
+//     ds_read_b64_tr_b16; in each 16-lane group lane j receives element j%4
+//     of the 8-byte pieces addressed by lanes 4r + j/4 (r = 0..3), so lanes
+//     address k-rows kbase + (j/4) at column offset 4*(j%4) and each lane
+//     gets 4 consecutive k of its own row (column).
+// Requires K % 64 == 0 and the contiguous extents % 8 == 0 (host-checked);
+// rows past M or N are loaded from a clamped address and never stored.
+// ===========================================================================
+namespace {
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+constexpr int kDBK = 64;
+
+template <int ROWS, bool KC, int NWAVES>
+struct DirectTile {
+    static constexpr int BYTES = ROWS * kDBK * 2;
+    static constexpr int NI = BYTES / 1024 / NWAVES;  // 1 KiB load instructions per wave per tile
+    static_assert(BYTES % (1024 * NWAVES) == 0, "tile must split into whole instructions per wave");
+    static_assert(KC || ROWS >= 64, "RC swizzle needs >= 8 chunks per k-row");
+    uint32_t goff[NI];
+
+    // grow0: first global row (m or n) of the tile; rows_total bounds it.
+    __device__ __forceinline__ void init(int wave, int lane, int64_t ld, int64_t grow0, int64_t rows_total) {
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int q = wave * NI + i;
+            if (KC) {
+                const int r = 8 * q + (lane >> 3);
+                const int c = (lane & 7) ^ (r & 7);
+                int64_t gr = grow0 + r;
+                if (gr > rows_total - 1) gr = rows_total - 1;
+                goff[i] = (uint32_t)(gr * ld + 8 * c);
+            } else {
+                constexpr int CPR = ROWS / 8;  // chunks per k-row
+                const int kr = q * (64 / CPR) + lane / CPR;
+                const int c = (lane % CPR) ^ (2 * (kr & 3));
+                int64_t gc = grow0 + 8 * c;
+                if (gc > rows_total - 8) gc = rows_total - 8;
+                goff[i] = (uint32_t)(kr * ld + gc);
+            }
+        }
+    }
+
+    // P advanced to the k-tile (KC: + k0, RC: + k0*ld); S = this operand's LDS tile.
+    __device__ __forceinline__ void issue(const unsigned short* P, unsigned short* S, int wave) const {
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+            __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)(P + goff[i]),
+                                             (__attribute__((address_space(3))) void*)(S + (wave * NI + i) * 512),
+                                             16, 0, 0);
+    }
+
+    // 8 bf16 (k = 16*st + 8*(lane/32) .. +7) of tile row r0 + lane%32.
+    __device__ __forceinline__ static bf16x8 frag(const unsigned short* S, int r0, int st, int lane) {
+        if (KC) {
+            const int row = r0 + (lane & 31);
+            const int slot = (2 * st + (lane >> 5)) ^ (row & 7);
+            return *(const bf16x8*)(S + row * kDBK + slot * 8);
+        } else {
+            const int G = lane >> 4, sp = lane & 15;
+            const int col = r0 + 16 * (G & 1) + 4 * (sp & 3);
+            s16x4 v[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int kr = 16 * st + 8 * (G >> 1) + 4 * h + (sp >> 2);
+                const int slot = (col >> 3) ^ (2 * (kr & 3));
+                v[h] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(S + kr * ROWS + slot * 8 + (col & 7)));
+            }
+            i16x8 w = {v[0][0], v[0][1], v[0][2], v[0][3], v[1][0], v[1][1], v[1][2], v[1][3]};
+            return __builtin_bit_cast(bf16x8, w);
+        }
+    }
+};
+
+// EPI: 0 store bf16, 1 bias + act then store bf16, 2 store fp32.
+template <int WAVES_M, int WAVES_N, bool AK, bool BKC, int EPI>
+__device__ __forceinline__ void gemm_bf16_direct_body(const GemmArgs& p) {
+    constexpr int BM = 256, BN = 256, NW = WAVES_M * WAVES_N;
+    constexpr int TM = BM / WAVES_M, TN = BN / WAVES_N, FM = TM / 32, FN = TN / 32;
+    using TA = DirectTile<BM, AK, NW>;
+    using TB = DirectTile<BN, BKC, NW>;
+    constexpr int A_EL = TA::BYTES / 2, B_EL = TB::BYTES / 2, STAGE = A_EL + B_EL;
+
+    __shared__ __attribute__((aligned(1024))) unsigned short smem[2 * STAGE];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+
+    int tm, tn;
+    tile_coords<8>(p.M, p.N, BM, BN, tm, tn);
+    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+
+    const unsigned short* A = (const unsigned short*)p.A;
+    const unsigned short* B = (const unsigned short*)p.B;
+    TA la;
+    TB lb;
+    la.init(wave, lane, p.lda, m0, p.M);
+    lb.init(wave, lane, p.ldb, n0, p.N);
+    const int64_t a_kstep = AK ? kDBK : (int64_t)kDBK * p.lda;
+    const int64_t b_kstep = BKC ? kDBK : (int64_t)kDBK * p.ldb;
+
+    f32x16 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+    const int nk = (int)(p.K / kDBK);
+    la.issue(A, smem, wave);
+    lb.issue(B, smem + A_EL, wave);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+
+    for (int kt = 0; kt < nk; ++kt) {
+        const int cur = kt & 1;
+        const unsigned short* As = smem + cur * STAGE;
+        const unsigned short* Bs = As + A_EL;
+        if (kt + 1 < nk) {
+            unsigned short* Ns = smem + (cur ^ 1) * STAGE;
+            la.issue(A + (int64_t)(kt + 1) * a_kstep, Ns, wave);
+            lb.issue(B + (int64_t)(kt + 1) * b_kstep, Ns + A_EL, wave);
+        }
+#pragma unroll
+        for (int st = 0; st < kDBK / 16; ++st) {
+            bf16x8 af[FM], bfr[FN];
+#pragma unroll
+            for (int i = 0; i < FM; ++i) af[i] = TA::frag(As, wm * TM + 32 * i, st, lane);
+#pragma unroll
+            for (int j = 0; j < FN; ++j) bfr[j] = TB::frag(Bs, wn * TN + 32 * j, st, lane);
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+    }
+
+    const int r = lane & 31, g = lane >> 5;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+        const int64_t n = n0 + wn * TN + 32 * j + r;
+        const bool nok = n < p.N;
+        const float bv = (EPI == 1 && p.bias != nullptr && nok) ? p.bias[n] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int64_t m = m0 + wm * TM + 32 * i + 8 * (v >> 2) + 4 * g + (v & 3);
+                if (nok && m < p.M) {
+                    float x = acc[i][j][v];
+                    if (EPI == 1) {
+                        if (p.bias != nullptr) x = x + bv;
+                        x = act_apply(x, p.act);
+                    }
+                    if (EPI == 2)
+                        ((float*)p.C)[m * p.ldc + n] = x;
+                    else
+                        ((unsigned short*)p.C)[m * p.ldc + n] = f32_to_bf16_rne(x);
+                }
+            }
+        }
+    }
+}
+
+}  // namespace
+
+#define C3_GEMM_BF16_D(NAME, WM, WN, AK, BKC, EPI)                                          \
+    extern "C" __global__ __launch_bounds__(64 * WM * WN) void NAME(GemmArgs p) {          \
+        gemm_bf16_direct_body<WM, WN, AK, BKC, EPI>(p);                                     \
+    }
+
+// fwd: X (KC) . W (RC) + bias, act -> bf16.  dx: dZ (KC) . W^T (KC) -> bf16.
+// dw: X^T (RC) . dZ (RC) -> fp32.  dwb: same, bf16 out.  tt: A^T (RC) . B^T (KC) -> bf16.
+// d256: 4 waves of 128x128; d256w8: 8 waves of 128x64.
+#define C3_GEMM_BF16_D_KINDS(T, WM, WN)                                  \
+    C3_GEMM_BF16_D(c3_gemm_bf16_fwd_##T, WM, WN, true, false, 1)         \
+    C3_GEMM_BF16_D(c3_gemm_bf16_dx_##T, WM, WN, true, true, 0)           \
+    C3_GEMM_BF16_D(c3_gemm_bf16_dw_##T, WM, WN, false, false, 2)         \
+    C3_GEMM_BF16_D(c3_gemm_bf16_dwb_##T, WM, WN, false, false, 0)        \
+    C3_GEMM_BF16_D(c3_gemm_bf16_tt_##T, WM, WN, false, true, 0)
+
+C3_GEMM_BF16_D_KINDS(d256, 2, 2)
+C3_GEMM_BF16_D_KINDS(d256w8, 2, 4)

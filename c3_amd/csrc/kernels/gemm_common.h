@@ -67,3 +67,27 @@ __device__ __forceinline__ unsigned short f32_to_bf16_rne(float x) {
 }
 
 __device__ __forceinline__ float bf16_to_f32(unsigned short h) { return __uint_as_float(((uint32_t)h) << 16); }
+
+// ---- bf16 bit-pattern helpers ----
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// bf16 bits: Y > 0 <=> sign clear, nonzero, not NaN (+inf counts as > 0).
+__device__ __forceinline__ bool bf16_gt0(unsigned short y) { return (short)y > 0 && y <= 0x7f80u; }
+
+// (Y > 0 ? 1 : 0) * dY on bf16 bit patterns: dY when Y > 0, else a zero with
+// dY's sign, or NaN when dY is Inf/NaN (0 * Inf = NaN).
+__device__ __forceinline__ unsigned short bf16_mask_mul(unsigned short y, unsigned short d) {
+    if (bf16_gt0(y)) return d;
+    if ((d & 0x7f80u) == 0x7f80u) return 0x7fc0u;
+    return d & 0x8000u;
+}
+
+__device__ __forceinline__ uint32_t mask_mul2(uint32_t y, uint32_t d) {
+    return (uint32_t)bf16_mask_mul((unsigned short)(y & 0xffff), (unsigned short)(d & 0xffff)) |
+           ((uint32_t)bf16_mask_mul((unsigned short)(y >> 16), (unsigned short)(d >> 16)) << 16);
+}
+
+__device__ __forceinline__ u32x4 mask_mul8(u32x4 y, u32x4 d) {
+    return u32x4{mask_mul2(y[0], d[0]), mask_mul2(y[1], d[1]), mask_mul2(y[2], d[2]), mask_mul2(y[3], d[3])};
+}
+

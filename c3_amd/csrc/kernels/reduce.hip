@@ -71,3 +71,40 @@ extern "C" __global__ __launch_bounds__(kThreads) void c3_rowsum_f32(
     for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
     if (lane == 0) out[row] = s;
 }
+
+// ---- bf16 backward pre-pass ----------------------------------------------
+// dZ = (Y > 0 ? 1 : 0) * dY on bf16 [M, N] (relu != 0; else dZ = dY), written
+// to dZ when non-null, and per-chunk column sums of dZ in fp32 into part
+// [nchunks, N] when non-null (the bias gradient, finished by
+// c3_colsum_final_f32).  One thread owns 8 consecutive columns (a 16-byte
+// vector) of a chunk of rows; consecutive threads cover consecutive vectors
+// of a row.  Requires N % 8 == 0 and 16-byte aligned rows.
+#include "gemm_common.h"
+
+extern "C" __global__ __launch_bounds__(kThreads) void c3_dz_colsum_bf16(
+    const unsigned short* __restrict__ Y, const unsigned short* __restrict__ dY, unsigned short* __restrict__ dZ,
+    float* __restrict__ part, int64_t M, int64_t N, int64_t rows_per_chunk, int relu) {
+    const int64_t v = (int64_t)blockIdx.x * kThreads + threadIdx.x;  // vector index within a row
+    if (8 * v >= N) return;
+    const int64_t chunk = blockIdx.y;
+    const int64_t r0 = chunk * rows_per_chunk;
+    const int64_t r1 = min(M, r0 + rows_per_chunk);
+    float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int64_t i = r0; i < r1; ++i) {
+        const int64_t off = i * N + 8 * v;
+        u32x4 d = *(const u32x4*)(dY + off);
+        if (relu) d = mask_mul8(*(const u32x4*)(Y + off), d);
+        if (dZ) *(u32x4*)(dZ + off) = d;
+        if (part) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                s[2 * e] += __uint_as_float(d[e] << 16);
+                s[2 * e + 1] += __uint_as_float(d[e] & 0xffff0000u);
+            }
+        }
+    }
+    if (part) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) part[chunk * N + 8 * v + e] = s[e];
+    }
+}

@@ -91,6 +91,25 @@ const Tile* choose_bf16_tile(int64_t M, int64_t N) {
     return &kBf16Tiles[0];
 }
 
+// Direct-to-LDS bf16 kernels (256x256 tiles, 64-deep k): plain operands
+// only (the backward masks are applied by the pre-pass), K % 64 == 0, and a
+// problem of at least 64 output tiles so the large tile fills the chip.
+const Tile kBf16Direct[] = {{"d256", 256, 256, 256}, {"d256w8", 256, 256, 512}};
+
+const Tile* choose_bf16_direct(Kind kind, const GemmArgs& a) {
+    if (kind == Kind::DxMask || kind == Kind::DwMask || a.db != nullptr) return nullptr;
+    if (a.K % 64 != 0 || a.K == 0) return nullptr;
+    if (a.M < 8 || a.N < 8) return nullptr;
+    const char* env = std::getenv("C3_HIP_GEMM_TILE_BF16");
+    if (env) {
+        if (const Tile* t = find_tile(kBf16Direct, 2, env)) return t;
+        return nullptr;  // an explicit non-direct tile was asked for
+    }
+    const int64_t blocks = ((a.M + 255) / 256) * ((a.N + 255) / 256);
+    if (blocks < 64) return nullptr;
+    return &kBf16Direct[1];
+}
+
 // bf16 kernels always move 16-byte vectors (8 elements): the contiguous
 // extent and the leading dimension must be multiples of 8.
 bool bf16_vec_ok(bool kc, int64_t rows, int64_t k, int64_t ld, const void* p, const void* pm) {
@@ -113,6 +132,13 @@ int run_gemm(int dtype, Kind kind, const GemmArgs& a0, bool a_kc, bool b_kc, hip
         if (!bf16_vec_ok(a_kc, a.M, a.K, a.lda, a.A, a.Amask) || !bf16_vec_ok(b_kc, a.N, a.K, a.ldb, a.B, a.Bmask))
             return set_error(C3HIP_ERR_UNSUPPORTED,
                              "bf16 GEMM needs 16-byte aligned operands and contiguous extents that are multiples of 8");
+        if (const Tile* d = choose_bf16_direct(kind, a)) {
+            char name[96];
+            std::snprintf(name, sizeof(name), "c3_gemm_bf16_%s_%s", kind_name(kind), d->name);
+            const int64_t blocks = ((a.M + 255) / 256) * ((a.N + 255) / 256);
+            void* args[] = {&a};
+            return launch(name, dim3((unsigned)blocks), dim3(d->threads), args, stream);
+        }
         const Tile* t = choose_bf16_tile(a.M, a.N);
         char name[96];
         std::snprintf(name, sizeof(name), "c3_gemm_bf16_%s_%s", kind_name(kind), t->name);
@@ -171,6 +197,74 @@ int colsum(const float* in, const float* mask, float* out, int64_t M, int64_t N,
     e = hipFreeAsync(part, stream);
     if (rc == C3HIP_OK && e != hipSuccess)
         rc = set_error(C3HIP_ERR_HIP, std::string("hipFreeAsync failed: ") + hipGetErrorString(e));
+    return rc;
+}
+
+// bf16 backward: one pass forms dZ = mask(Y) * dY in bf16 (stream-ordered
+// workspace) together with the per-chunk column sums for db, then dX and dW
+// run as plain bf16 GEMMs on dZ (the direct-to-LDS kernels cannot apply the
+// mask while loading).  Without ReLU, dZ is dY itself.
+int linear_bwd_bf16(const void* X, const void* W, const void* Y, const void* dY, void* dX, float* dW, float* db,
+                    int64_t M, int64_t K, int64_t N, bool relu, hipStream_t stream) {
+    if (M == 0 || N == 0) {
+        if (db && N > 0) {
+            hipError_t e = hipMemsetAsync(db, 0, (size_t)N * sizeof(float), stream);
+            if (e != hipSuccess) return set_error(C3HIP_ERR_HIP, std::string("hipMemsetAsync: ") + hipGetErrorString(e));
+        }
+        if (dW && K > 0 && N > 0) {
+            hipError_t e = hipMemsetAsync(dW, 0, (size_t)(K * N) * sizeof(float), stream);
+            if (e != hipSuccess) return set_error(C3HIP_ERR_HIP, std::string("hipMemsetAsync: ") + hipGetErrorString(e));
+        }
+        if (dX && M > 0 && K > 0) {
+            hipError_t e = hipMemsetAsync(dX, 0, (size_t)(M * K) * 2, stream);
+            if (e != hipSuccess) return set_error(C3HIP_ERR_HIP, std::string("hipMemsetAsync: ") + hipGetErrorString(e));
+        }
+        return C3HIP_OK;
+    }
+    if (N % 8 != 0 || !aligned16(Y) || !aligned16(dY))
+        return set_error(C3HIP_ERR_UNSUPPORTED, "bf16 backward needs N % 8 == 0 and 16-byte aligned Y, dY");
+    const bool need_dz = relu && (dX || dW);
+    int64_t nchunks = std::min<int64_t>(256, std::max<int64_t>(1, (M + 31) / 32));
+    int64_t rows_per_chunk = (M + nchunks - 1) / nchunks;
+    nchunks = (M + rows_per_chunk - 1) / rows_per_chunk;
+    void* dz = nullptr;
+    float* part = nullptr;
+    int rc = C3HIP_OK;
+    hipError_t e;
+    if (need_dz && (e = hipMallocAsync(&dz, (size_t)(M * N) * 2, stream)) != hipSuccess)
+        return set_error(C3HIP_ERR_HIP, std::string("hipMallocAsync(dZ): ") + hipGetErrorString(e));
+    if (db && nchunks > 1 && (e = hipMallocAsync((void**)&part, (size_t)(nchunks * N) * sizeof(float), stream)) != hipSuccess) {
+        if (dz) (void)hipFreeAsync(dz, stream);
+        return set_error(C3HIP_ERR_HIP, std::string("hipMallocAsync(partials): ") + hipGetErrorString(e));
+    }
+    if (need_dz || db) {
+        float* part_out = db ? (nchunks > 1 ? part : db) : nullptr;
+        int relu_i = relu ? 1 : 0;
+        const unsigned gx = (unsigned)((N / 8 + 255) / 256);
+        void* args[] = {(void*)&Y, (void*)&dY, &dz, &part_out, &M, &N, &rows_per_chunk, &relu_i};
+        rc = launch("c3_dz_colsum_bf16", dim3(gx, (unsigned)nchunks), dim3(256), args, stream);
+        if (rc == C3HIP_OK && db && nchunks > 1) {
+            void* args2[] = {(void*)&part, (void*)&db, &nchunks, &N};
+            rc = launch("c3_colsum_final_f32", dim3((unsigned)((N + 255) / 256)), dim3(256), args2, stream);
+        }
+    }
+    const void* dzp = need_dz ? dz : dY;
+    if (rc == C3HIP_OK && dX) {
+        GemmArgs a{};
+        a.A = dzp; a.B = W; a.C = dX;
+        a.M = M; a.N = K; a.K = N;
+        a.lda = N; a.ldb = N; a.ldc = K;
+        rc = run_gemm(C3HIP_BF16, Kind::Dx, a, true, true, stream);
+    }
+    if (rc == C3HIP_OK && dW) {
+        GemmArgs a{};
+        a.A = X; a.B = dzp; a.C = dW;
+        a.M = K; a.N = N; a.K = M;
+        a.lda = K; a.ldb = N; a.ldc = N;
+        rc = run_gemm(C3HIP_BF16, Kind::Dw, a, false, false, stream);
+    }
+    if (dz) (void)hipFreeAsync(dz, stream);
+    if (part) (void)hipFreeAsync(part, stream);
     return rc;
 }
 
@@ -264,6 +358,7 @@ int c3hip_linear_bwd(int dtype, const void* X, const void* W, const void* Y, con
     if (M > 0 && N > 0 && (!dY || (relu && !Y))) return set_error(C3HIP_ERR_INVALID, "null dY / Y");
     if (dX && K > 0 && M > 0 && N > 0 && !W) return set_error(C3HIP_ERR_INVALID, "dX needs W");
     if (dW && K > 0 && N > 0 && M > 0 && !X) return set_error(C3HIP_ERR_INVALID, "dW needs X");
+    if (dtype == C3HIP_BF16) return linear_bwd_bf16(X, W, Y, dY, dX, dW, db, M, K, N, relu, stream);
     const void* mask = relu ? Y : nullptr;
     if (dX) {
         // dX[M,K] = dZ[M,N] . W^T : logical (M, N=K, K=N), A = dY (k-contig), B(k=n, j) = W[j*N + n].
