@@ -332,12 +332,21 @@ struct DirectTile {
     }
 
     // P advanced to the k-tile (KC: + k0, RC: + k0*ld); S = this operand's LDS tile.
+    // The loads are issued through inline asm (M0 = LDS destination of the
+    // instruction, wave-uniform): the compiler then does not treat them as
+    // LDS writes that every later LDS read must wait for.  The kernel orders
+    // them itself: a stage is only read after s_waitcnt vmcnt(0) and a
+    // barrier, and only refilled after the barrier that ends its last read.
     __device__ __forceinline__ void issue(const unsigned short* P, unsigned short* S, int wave) const {
 #pragma unroll
-        for (int i = 0; i < NI; ++i)
-            __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)(P + goff[i]),
-                                             (__attribute__((address_space(3))) void*)(S + (wave * NI + i) * 512),
-                                             16, 0, 0);
+        for (int i = 0; i < NI; ++i) {
+            const uint32_t lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)(S + (wave * NI + i) * 512);
+            const unsigned short* src = P + goff[i];
+            asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+                         :
+                         : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(src)
+                         : "memory", "m0");
+        }
     }
 
     // 8 bf16 (k = 16*st + 8*(lane/32) .. +7) of tile row r0 + lane%32.
