@@ -26,12 +26,17 @@
 namespace {
 
 constexpr int kBK = 16;   // k depth of one LDS stage
-constexpr int kPad = 4;   // floats of padding per LDS row (keeps 16-byte alignment)
+constexpr int kPad = 4;   // floats of padding per k-row of a row-contiguous tile
 
+// LDS tile layouts.  KC (k contiguous in global): [ROWS][16 k], 64 B per row,
+// the 16-byte chunk holding k 4c..4c+3 of row r stored in slot
+// c ^ ((r >> 1) & 3), so the 16-byte fragment reads of 8 consecutive rows
+// touch 8 distinct bank groups.  !KC: [16 k][ROWS + 4].
 template <int ROWS, bool KC>
 struct Lds {
-    static constexpr int STRIDE = KC ? (kBK + kPad) : (ROWS + kPad);
+    static constexpr int STRIDE = KC ? kBK : (ROWS + kPad);
     static constexpr int SIZE = KC ? ROWS * STRIDE : kBK * STRIDE;
+    __device__ __forceinline__ static int kc_slot(int row, int chunk) { return chunk ^ ((row >> 1) & 3); }
 };
 
 // Global -> register staging of one operand tile (ROWS x kBK logical, ROWS =
@@ -107,7 +112,7 @@ struct TileLoader {
         for (int i = 0; i < NV; ++i) {
             const int rr = KC ? row0 + i * RSTEP : row0;
             const int kk = KC ? kk0 : kk0 + i * KSTEP;
-            const int off = KC ? rr * STRIDE + kk : kk * STRIDE + rr;
+            const int off = KC ? rr * STRIDE + 4 * Lds<ROWS, KC>::kc_slot(rr, kk >> 2) : kk * STRIDE + rr;
             *(f32x4*)(S + off) = r[i];
         }
     }
@@ -120,7 +125,8 @@ __device__ __forceinline__ void read_frag(const float* __restrict__ S, int r0, i
     const int r = lane & 31, g = lane >> 5;
     constexpr int STRIDE = Lds<ROWS, KC>::STRIDE;
     if (KC) {
-        const f32x4 v = *(const f32x4*)(S + (r0 + r) * STRIDE + 8 * g + 4 * h);
+        const int row = r0 + r;
+        const f32x4 v = *(const f32x4*)(S + row * STRIDE + 4 * Lds<ROWS, KC>::kc_slot(row, 2 * g + h));
         f[0] = v[0]; f[1] = v[1]; f[2] = v[2]; f[3] = v[3];
     } else {
 #pragma unroll

@@ -102,7 +102,7 @@ const Tile* choose_bf16_direct(Kind kind, const GemmArgs& a) {
     if (a.M < 8 || a.N < 8) return nullptr;
     const char* env = std::getenv("C3_HIP_GEMM_TILE_BF16");
     if (env) {
-        if (const Tile* t = find_tile(kBf16Direct, 2, env)) return t;
+        if (const Tile* t = find_tile(kBf16Direct, sizeof(kBf16Direct) / sizeof(kBf16Direct[0]), env)) return t;
         return nullptr;  // an explicit non-direct tile was asked for
     }
     const int64_t blocks = ((a.M + 255) / 256) * ((a.N + 255) / 256);
