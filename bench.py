@@ -42,7 +42,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-extras", action="store_true", help="skip the bf16 and elementwise evidence lines")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the evidence beside the headline (bf16 layer and sweep, elementwise, MLP steps)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain copy-like stream (scale: read 2^26 fp32, write 2^26 fp32) three times; "
                          "its FETCH_SIZE/WRITE_SIZE counters calibrate the HBM traffic figures")
@@ -161,7 +162,13 @@ def main():
     }
     if not args.no_extras:
         out["bf16"] = bench_bf16(torch, C, dev, s, args)
-        out["elementwise"] = bench_elementwise(torch, C, dev, s)
+        out["bf16_sweep"] = bench_bf16_sweep(torch, C, dev, s)
+        out["elementwise"] = {"2^28": bench_elementwise(torch, C, dev, s, 1 << 28, sets=1),
+                              "2^24": bench_elementwise(torch, C, dev, s, 1 << 24, sets=8)}
+        out["mlp_784_256_128_10_fp32"] = bench_mlp(torch, C, dev, s, [784, 256, 128, 10], 128, C.F32,
+                                                   steps=200, uniform_x=True)
+        out["mlp_deep_bf16"] = bench_mlp(torch, C, dev, s, [4096, 8192, 8192, 8192, 4096, 1000], 16384, C.BF16,
+                                         steps=10, uniform_x=False)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out), flush=True)
@@ -213,29 +220,135 @@ def bench_bf16(torch, C, dev, s, args):
             "tflops": round(tf, 2), "frac_of_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4)}
 
 
-def bench_elementwise(torch, C, dev, s, n=1 << 28, iters=10):
-    """The eight elementwise ops over 2^28 fp32 elements (1 GiB per operand, far
-    above the 256 MB Infinity Cache), algorithmic bytes: 12 B/elem binary,
-    8 B/elem unary."""
-    a = torch.randn(n, device=dev)
-    bb = torch.rand(n, device=dev) * 1.5 + 0.5
-    o = torch.empty(n, device=dev)
+def bench_elementwise(torch, C, dev, s, n, sets, iters=10):
+    """The eight elementwise ops over n fp32 elements.  Algorithmic bytes:
+    12 B/elem binary, 8 B/elem unary.  With sets > 1 the launches rotate over
+    that many operand sets so that each launch reads memory the previous ones
+    did not touch (2^24 elements: 8 sets of 192 MiB, above the 256 MB
+    Infinity Cache)."""
+    bufs = [(torch.randn(n, device=dev), torch.rand(n, device=dev) * 1.5 + 0.5, torch.empty(n, device=dev))
+            for _ in range(sets)]
     res = {}
     for name, code in C.EW_OPS.items():
         nbytes = (12 if code in (C.EW_ADD, C.EW_SUB, C.EW_MUL, C.EW_DIV, C.EW_RELU_BWD) else 8) * n
-        fn = lambda: C.elementwise(code, C.F32, a.data_ptr(), bb.data_ptr(), 0.5, o.data_ptr(), n, 0, s)  # noqa
-        fn()
+
+        def fn(i):
+            a, bb, o = bufs[i % sets]
+            C.elementwise(code, C.F32, a.data_ptr(), bb.data_ptr(), 0.5, o.data_ptr(), n, 0, s)
+
+        for i in range(sets):
+            fn(i)
+        total = iters * sets
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         e0.record()
-        for _ in range(iters):
-            fn()
+        for i in range(total):
+            fn(i)
         e1.record()
         torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1) / iters
+        ms = e0.elapsed_time(e1) / total
         gbs = nbytes / (ms * 1e-3) / 1e9
         res[name] = {"GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
-    return {"n": n, "ops": res}
+    del bufs
+    torch.cuda.empty_cache()
+    return {"n": n, "operand_sets": sets, "ops": res}
+
+
+SWEEP = [(m, k, n) for m in (1024, 4096, 16384) for k in (1024, 4096, 8192) for n in (1024, 4096, 8192)]
+
+
+def bench_bf16_sweep(torch, C, dev, s, reps=5):
+    """bf16 Linear+bias+ReLU forward + fused backward over the M x K x N sweep
+    {1024, 4096, 16384} x {1024, 4096, 8192} x {1024, 4096, 8192}: TFLOP/s of
+    the step (6 M N K flop) per shape, events around `reps` back-to-back steps."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(0x5EE9)
+    res = {}
+    for (m, k, n) in SWEEP:
+        X = torch.randn(m, k, device=dev, generator=g).to(torch.bfloat16)
+        W = (torch.randn(k, n, device=dev, generator=g) / float(k) ** 0.5).to(torch.bfloat16)
+        b = torch.randn(n, device=dev, generator=g) * 0.1
+        dY = torch.randn(m, n, device=dev, generator=g).to(torch.bfloat16)
+        Y = torch.empty(m, n, device=dev, dtype=torch.bfloat16)
+        dX = torch.empty(m, k, device=dev, dtype=torch.bfloat16)
+        dW = torch.empty(k, n, device=dev)
+        db = torch.empty(n, device=dev)
+
+        def step():
+            C.linear_fwd(C.BF16, X.data_ptr(), W.data_ptr(), b.data_ptr(), Y.data_ptr(), m, k, n, C.ACT_RELU, s)
+            C.linear_bwd(C.BF16, X.data_ptr(), W.data_ptr(), Y.data_ptr(), dY.data_ptr(), dX.data_ptr(),
+                         dW.data_ptr(), db.data_ptr(), m, k, n, C.ACT_RELU, s)
+
+        step()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(reps):
+            step()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        res[f"{m}x{k}x{n}"] = round(6.0 * m * n * k / (ms * 1e-3) / 1e12, 1)
+        del X, W, b, dY, Y, dX, dW, db
+    torch.cuda.empty_cache()
+    vals = sorted(res.values())
+    return {"workload": "bf16 Linear+bias+ReLU fwd+bwd step per shape, TFLOP/s", "tflops": res,
+            "median_tflops": vals[len(vals) // 2], "min_tflops": vals[0], "max_tflops": vals[-1]}
+
+
+def bench_mlp(torch, C, dev, s, dims, batch, dtype, steps, uniform_x):
+    """Train step of an MLP (ReLU between layers, softmax-CE, SGD) through the
+    dispatch flow (c3_amd/trainer.py: region kernels from RegionFusionRegistry,
+    fused backwards from C3BackwardCapture, JIT cache warm), after warm-up
+    until every layer runs on an installed kernel.  Flop per step: 6 * batch
+    * sum(K*N) (forward 2x, backward 4x including the first layer's dX)."""
+    from c3_amd import trainer as T
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(0xC3)
+    tr = T.MlpTrainer(dims, batch, dtype)
+    keep = []
+    for l in range(len(dims) - 1):
+        bound = (6.0 / dims[l]) ** 0.5
+        w = (torch.rand(dims[l], dims[l + 1], device=dev, generator=g) * 2 - 1) * bound
+        wp, bp = tr.params(l)
+        C.cast(C.F32, dtype, w.data_ptr(), wp, w.numel(), s)  # biases stay zero
+        keep.append(w)
+    x = torch.rand(batch, dims[0], device=dev, generator=g) if uniform_x else \
+        torch.randn(batch, dims[0], device=dev, generator=g)
+    xd = x if dtype == C.F32 else x.to(torch.bfloat16)
+    lbl = torch.randint(0, dims[-1], (batch,), device=dev, generator=g, dtype=torch.int32)
+    torch.cuda.synchronize()
+    lr = 1e-3
+    warm = tr.warm_up(xd.data_ptr(), lbl.data_ptr(), lr, 16, s)
+    st0 = tr.stats()
+    loss0 = tr.step(xd.data_ptr(), lbl.data_ptr(), lr, True, s)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(steps):
+        tr.step(xd.data_ptr(), lbl.data_ptr(), lr, False, s)
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_time(e1) / steps
+    loss1 = tr.step(xd.data_ptr(), lbl.data_ptr(), lr, True, s)
+    st1 = tr.stats()
+    tr.close()
+    del keep, x, xd, lbl
+    torch.cuda.empty_cache()
+    flop = 6.0 * batch * sum(dims[l] * dims[l + 1] for l in range(len(dims) - 1))
+    tf = flop / (ms * 1e-3) / 1e12
+    peak = PEAK_FP32_TFLOPS if dtype == C.F32 else PEAK_BF16_TFLOPS
+    return {"dims": dims, "batch": batch, "dtype": "fp32" if dtype == C.F32 else "bf16",
+            "ms_per_step": round(ms, 4), "us_per_step_wall": round(wall / steps * 1e6, 1),
+            "tflops": round(tf, 3), "frac_of_peak": round(tf / peak, 4), "flop_per_step": flop,
+            "warm_up_steps": warm, "region_hits_timed": st1["region_hits"] - st0["region_hits"],
+            "backward_hits_timed": st1["backward_hits"] - st0["backward_hits"],
+            "eager_ops_timed": st1["eager_ops"] - st0["eager_ops"],
+            "fully_dispatched": bool(st1["fully_dispatched"]),
+            "loss_before": round(loss0, 5), "loss_after": round(loss1, 5)}
 
 
 def cpu_baseline():
@@ -265,12 +378,58 @@ def cpu_baseline():
     t3 = time.perf_counter()
     flop = 2.0 * rows * N * K * 2 + 2.0 * rows * M * N
     secs = t3 - t0
-    del np
     return {"value": round(flop / secs / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
             "sample": f"oracle on {rows} rows of Y ({t1 - t0:.1f}s), {rows} rows of dX ({t2 - t1:.1f}s) and "
                       f"{rows} rows of dW ({t3 - t2:.1f}s) of the {M}x{K}x{N} layer, one core; "
                       f"full fwd+bwd step extrapolates to {6.0 * M * N * K / (flop / secs) / 3600:.1f} h",
-            "host_cpu": _cpu_model()}
+            "host_cpu": _cpu_model(),
+            "mlp_784_256_128_10_fp32": _cpu_mlp(O, np),
+            "elementwise_2^24": _cpu_elementwise(O, np)}
+
+
+def _cpu_mlp(O, np, reps=5):
+    """One full train step of the 784-256-128-10 MLP (batch 128) in the
+    oracle on one core: forward, softmax-CE, backward, SGD; median of reps."""
+    dims, B = [784, 256, 128, 10], 128
+    X = O.uniform(1, (B, 784))
+    Ws = [O.uniform(2 + l, (dims[l], dims[l + 1]), -(6.0 / dims[l]) ** 0.5, (6.0 / dims[l]) ** 0.5)
+          for l in range(3)]
+    bs = [np.zeros(dims[l + 1], np.float32) for l in range(3)]
+    lbl = O.labels(9, B, 10)
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        acts = [X]
+        for l in range(3):
+            acts.append(O.linear_fwd(acts[-1], Ws[l], bs[l], 1 if l < 2 else 0))
+        _, g = O.softmax_ce(acts[3], lbl)
+        for l in reversed(range(3)):
+            g, dW, db = O.linear_bwd(acts[l], Ws[l], acts[l + 1], g, 1 if l < 2 else 0)
+            O.sgd_update(Ws[l], dW, 1e-3)
+            O.sgd_update(bs[l], db, 1e-3)
+        times.append(time.perf_counter() - t0)
+    ms = sorted(times)[reps // 2] * 1e3
+    flop = 6.0 * B * sum(dims[l] * dims[l + 1] for l in range(3))
+    return {"ms_per_step": round(ms, 3), "tflops": round(flop / (ms * 1e-3) / 1e12, 6), "cores": 1,
+            "kind": "port", "sample": f"median of {reps} full steps"}
+
+
+def _cpu_elementwise(O, np, n=1 << 24, reps=3):
+    """Oracle elementwise ops over 2^24 fp32 elements on one core (GB/s of
+    algorithmic traffic, median of reps)."""
+    a = O.normal(1, n)
+    b = O.uniform(2, n, 0.5, 2.0)
+    res = {}
+    for name, code in (("add", O.EW_ADD), ("div", O.EW_DIV), ("relu", O.EW_RELU), ("relu_bwd", O.EW_RELU_BWD)):
+        binary = code in O.EW_BINARY
+        times = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            O.elementwise(code, a, b if binary else None, alpha=0.5)
+            times.append(time.perf_counter() - t0)
+        sec = sorted(times)[reps // 2]
+        res[name] = round((12 if binary else 8) * n / sec / 1e9, 2)
+    return {"GB/s": res, "cores": 1, "kind": "port", "sample": f"n = 2^24, median of {reps}"}
 
 
 def _cpu_model():

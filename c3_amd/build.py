@@ -32,8 +32,8 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 NO_PACKED_FP32 = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 DEVICE_FLAGS = ["--genco", "--no-gpu-bundle-output", f"--offload-arch={ARCH}", "-O3", "-std=c++17", *NO_PACKED_FP32]
 
-KERNELS = ["elementwise", "gemm_f32", "gemm_bf16", "reduce"]
-RUNTIME_SOURCES = ["runtime/c3hip_runtime.cpp", "runtime/c3hip_ops.cpp"]
+KERNELS = ["elementwise", "gemm_f32", "gemm_bf16", "reduce", "loss"]
+RUNTIME_SOURCES = ["runtime/c3hip_runtime.cpp", "runtime/c3hip_ops.cpp", "runtime/c3hip_loss.cpp"]
 HOST_SOURCES = sorted(p.name for p in (CSRC / "host" / "src").glob("*.cpp"))
 TESTS_CPP = ROOT / "tests" / "cpp"
 

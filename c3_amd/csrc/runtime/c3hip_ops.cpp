@@ -296,7 +296,7 @@ int c3hip_elementwise(int op, int dtype, const void* a, const void* b, float alp
     if (vec) {
         std::snprintf(name, sizeof(name), "c3_ew_%s_f32_v", nm);
         int64_t n4 = n / 4, bmod4 = bmod / 4;
-        const int64_t per_block = 256 * 4;
+        const int64_t per_block = 256;  // one vector per thread (elementwise.hip kUnroll)
         const int64_t blocks = (n4 + per_block - 1) / per_block;
         if (blocks > 0x7fffffff) return set_error(C3HIP_ERR_TOO_LARGE, "elementwise grid too large");
         void* args[] = {(void*)&a, (void*)&b, &alpha, &out, &n4, &bmod4};

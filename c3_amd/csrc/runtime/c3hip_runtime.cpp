@@ -41,7 +41,7 @@ struct DeviceState {
 std::mutex g_mu;
 std::unordered_map<int, std::unique_ptr<DeviceState>> g_devices;
 
-const char* const kModuleNames[] = {"elementwise", "gemm_f32", "gemm_bf16", "reduce"};
+const char* const kModuleNames[] = {"elementwise", "gemm_f32", "gemm_bf16", "reduce", "loss"};
 
 bool known_module(const std::string& name) {
     for (const char* m : kModuleNames)

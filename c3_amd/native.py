@@ -38,6 +38,9 @@ SIGNATURES = {
     "c3hip_linear_fwd": (_int, [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _vp]),
     "c3hip_linear_bwd": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _vp]),
     "c3hip_sum_reduce": (_int, [_vp, _vp, _i64, _i64, _int, _vp]),
+    "c3hip_softmax_ce": (_int, [_int, _vp, _vp, _vp, _vp, _i64, _i64, _vp]),
+    "c3hip_cast": (_int, [_int, _int, _vp, _vp, _i64, _vp]),
+    "c3hip_sgd_update": (_int, [_int, _vp, _vp, _f, _i64, _vp]),
 }
 
 
@@ -114,3 +117,16 @@ def linear_bwd(dtype: int, X: int | None, W: int | None, Y: int | None, dY: int,
 
 def sum_reduce(inp: int, out: int, M: int, N: int, axis: int = 0, stream: int = 0) -> None:
     _check("c3hip_sum_reduce", load().c3hip_sum_reduce(inp, out, M, N, axis, stream))
+
+
+def softmax_ce(dtype: int, logits: int, labels: int, loss_rows: int | None, dlogits: int | None, M: int, C: int,
+               stream: int = 0) -> None:
+    _check("c3hip_softmax_ce", load().c3hip_softmax_ce(dtype, logits, labels, loss_rows, dlogits, M, C, stream))
+
+
+def cast(src_dtype: int, dst_dtype: int, inp: int, out: int, n: int, stream: int = 0) -> None:
+    _check("c3hip_cast", load().c3hip_cast(src_dtype, dst_dtype, inp, out, n, stream))
+
+
+def sgd_update(dtype: int, w: int, g: int, lr: float, n: int, stream: int = 0) -> None:
+    _check("c3hip_sgd_update", load().c3hip_sgd_update(dtype, w, g, lr, n, stream))

@@ -78,7 +78,7 @@ int c3hip_shutdown(void);
 
 /*
  * Register a code object image for module `module_name` ("elementwise",
- * "gemm_f32", "gemm_bf16" or "reduce") on the current device, e.g. one read
+ * "gemm_f32", "gemm_bf16", "reduce" or "loss") on the current device, e.g. one read
  * back from the on-disk JIT cache.  A module already loaded on the device is
  * kept (returns 0); later lookups use whichever image was loaded first.
  * Replaces the reference's JITCache read path, which reloads cached LLVM
@@ -153,6 +153,39 @@ int c3hip_linear_bwd(int dtype, const void* X, const void* W, const void* Y, con
  * for axis 0 (grown on demand, freed by c3hip_shutdown).
  */
 int c3hip_sum_reduce(const float* in, float* out, int64_t M, int64_t N, int axis, void* stream);
+
+/*
+ * Softmax cross-entropy over the M rows of logits[M,C] (C3HIP_F32: fp32;
+ * C3HIP_BF16: bf16) with int32 labels in [0, C):
+ *   loss_rows[i]  = logsumexp(logits[i,:]) - logits[i, labels[i]]   (fp32)
+ *   dlogits[i,j]  = (softmax(logits[i,:])_j - [j == labels[i]]) / M  (logits' dtype)
+ * loss_rows or dlogits may be NULL.  C <= 2048.  A label outside [0, C)
+ * gives NaN in that row.  The mean loss is the row sum of loss_rows over M
+ * (c3hip_sum_reduce with axis 1 on a [1, M] view).
+ * The reference has no kernel for this step: the host framework's CE op
+ * (op code 79, src/C3/RollingHash.cpp:66) runs between the fused forward and
+ * the backward of the MLP train step; it is here so the whole step stays on
+ * the device.
+ */
+int c3hip_softmax_ce(int dtype, const void* logits, const int32_t* labels, float* loss_rows, void* dlogits,
+                     int64_t M, int64_t C, void* stream);
+
+/*
+ * Element type conversion of n contiguous elements: C3HIP_F32 -> C3HIP_BF16
+ * (round to nearest-even, NaN stays NaN) or C3HIP_BF16 -> C3HIP_F32 (exact).
+ * The same dtype on both sides is a device copy.  No reference counterpart
+ * (the reference is fp32 only); it prepares bf16 operands on the device.
+ */
+int c3hip_cast(int src_dtype, int dst_dtype, const void* in, void* out, int64_t n, void* stream);
+
+/*
+ * SGD step on a parameter of n elements: w = w - lr * g, with g fp32 and the
+ * product rounded before the subtraction (no fused multiply-add).
+ * dtype C3HIP_BF16: w is bf16, updated in fp32 and rounded back.  The
+ * optimizer belongs to the host framework in the reference (not part of C3);
+ * it closes the train step on the device.
+ */
+int c3hip_sgd_update(int dtype, void* w, const float* g, float lr, int64_t n, void* stream);
 
 #ifdef __cplusplus
 }

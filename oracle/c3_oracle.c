@@ -243,12 +243,13 @@ void oracle_elementwise(int op, const float* a, const float* b, float alpha, flo
     }
 }
 
-/* Mean softmax cross-entropy over M rows of C logits, and its gradient
- * dlogits = (softmax - onehot) / M.  The reference leaves this step to the
- * host framework's CE op (op code 79 in src/C3/RollingHash.cpp:66); it is
- * here so train-step tests have a checker.  exp/log come from libm.        */
-float oracle_softmax_ce(const float* logits, const int32_t* labels, float* dlogits, int64_t M,
-                        int64_t C) {
+/* Mean softmax cross-entropy over M rows of C logits, its per-row terms
+ * loss_rows[i] = logsumexp(row i) - row_i[label_i] (nullable) and its gradient
+ * dlogits = (softmax - onehot) / M (nullable).  The reference leaves this
+ * step to the host framework's CE op (op code 79 in src/C3/RollingHash.cpp:66);
+ * it is here so train-step tests have a checker.  exp/log come from libm.  */
+float oracle_softmax_ce(const float* logits, const int32_t* labels, float* loss_rows, float* dlogits,
+                        int64_t M, int64_t C) {
     double loss = 0.0;
     float inv_m = 1.0f / (float)M;
     for (int64_t i = 0; i < M; ++i) {
@@ -258,7 +259,9 @@ float oracle_softmax_ce(const float* logits, const int32_t* labels, float* dlogi
         float s = 0.0f;
         for (int64_t j = 0; j < C; ++j) s = s + expf(row[j] - mx);
         float lse = mx + logf(s);
-        loss += (double)(lse - row[labels[i]]);
+        float li = lse - row[labels[i]];
+        if (loss_rows) loss_rows[i] = li;
+        loss += (double)li;
         if (dlogits) {
             for (int64_t j = 0; j < C; ++j) {
                 float p = expf(row[j] - mx) / s;
@@ -268,4 +271,25 @@ float oracle_softmax_ce(const float* logits, const int32_t* labels, float* dlogi
         }
     }
     return (float)(loss / (double)M);
+}
+
+/* SGD step w = w - lr * g with the product rounded first (no FMA; this file
+ * is built with -ffp-contract=off).  The optimizer is the host framework's in
+ * the reference; this is the checker of the device update.  */
+void oracle_sgd_update(float* w, const float* g, float lr, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) {
+        float step = lr * g[i];
+        w[i] = w[i] - step;
+    }
+}
+
+/* The same on bf16 bit patterns: widen, update in fp32, round to nearest-even. */
+void oracle_sgd_update_bf16(uint16_t* w, const float* g, float lr, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) {
+        uint32_t u = (uint32_t)w[i] << 16;
+        float x;
+        memcpy(&x, &u, 4);
+        float step = lr * g[i];
+        w[i] = oracle_f32_to_bf16(x - step);
+    }
 }

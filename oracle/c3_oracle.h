@@ -62,8 +62,10 @@ void oracle_elementwise(int op, const float* a, const float* b, float alpha, flo
                         int64_t n, int64_t bmod);
 
 /* ---- softmax cross-entropy for the MLP train step (host-side step of the caller) ---- */
-float oracle_softmax_ce(const float* logits, const int32_t* labels, float* dlogits, int64_t M,
-                        int64_t C);
+float oracle_softmax_ce(const float* logits, const int32_t* labels, float* loss_rows, float* dlogits,
+                        int64_t M, int64_t C);
+void oracle_sgd_update(float* w, const float* g, float lr, int64_t n);
+void oracle_sgd_update_bf16(uint16_t* w, const float* g, float lr, int64_t n);
 
 #ifdef __cplusplus
 }

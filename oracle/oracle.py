@@ -48,8 +48,10 @@ def lib():
         vp = ctypes.c_void_p
         L.oracle_linear_bwd.argtypes = [_f32p, _f32p, _f32p, _f32p, vp, vp, vp, _i64, _i64, _i64, ctypes.c_int]
         L.oracle_elementwise.argtypes = [ctypes.c_int, _f32p, vp, ctypes.c_float, _f32p, _i64, _i64]
-        L.oracle_softmax_ce.argtypes = [_f32p, _i32p, vp, _i64, _i64]
+        L.oracle_softmax_ce.argtypes = [_f32p, _i32p, vp, vp, _i64, _i64]
         L.oracle_softmax_ce.restype = ctypes.c_float
+        L.oracle_sgd_update.argtypes = [_f32p, _f32p, ctypes.c_float, _i64]
+        L.oracle_sgd_update_bf16.argtypes = [_u16p, _f32p, ctypes.c_float, _i64]
         _lib = L
     return _lib
 
@@ -171,10 +173,25 @@ def elementwise(op, a, b=None, alpha=0.0, bmod=0):
     return out
 
 
-def softmax_ce(logits, lbl, want_grad=True):
+def softmax_ce(logits, lbl, want_grad=True, want_rows=False):
+    """Mean CE loss and dlogits (None unless want_grad); with want_rows the
+    per-row losses are returned as a third value."""
     logits = _c(logits)
     lbl = np.ascontiguousarray(lbl, dtype=np.int32)
     M, C = logits.shape
     d = np.empty_like(logits) if want_grad else None
-    loss = lib().oracle_softmax_ce(logits.reshape(-1), lbl, _ptr(d), M, C)
-    return loss, d
+    rows = np.empty(M, dtype=np.float32) if want_rows else None
+    loss = lib().oracle_softmax_ce(logits.reshape(-1), lbl, _ptr(rows), _ptr(d), M, C)
+    return (loss, d, rows) if want_rows else (loss, d)
+
+
+def sgd_update(w, g, lr):
+    """w - lr * g (product rounded first); w fp32 values, or bf16 bit patterns (uint16)."""
+    g = _c(g).reshape(-1)
+    if np.asarray(w).dtype == np.uint16:
+        out = np.array(w, dtype=np.uint16, copy=True)
+        lib().oracle_sgd_update_bf16(out.reshape(-1), g, lr, out.size)
+        return out
+    out = np.array(_c(w), copy=True)
+    lib().oracle_sgd_update(out.reshape(-1), g, lr, out.size)
+    return out

@@ -93,3 +93,35 @@ def mask_flips(y_got, z_ref, band):
     outside = diff & (np.abs(z_ref) > band)
     assert not outside.any(), f"{int(outside.sum())} mask flips outside the rounding band"
     return int(diff.sum())
+
+
+def ce_bounds(logits, lbl, d_ref):
+    """Per-element bounds of a softmax-CE against the oracle: exp/log within a
+    few ulp on either side and a reordered row sum give, with C classes,
+      loss_i:  2 (C + 8) u + 4 u (|max_i| + |lse_i| + |x_{i,y}|)
+      dlogit:  (2 (C + 8) u p_ij + 2 u) / M        (p = softmax)."""
+    M, C = logits.shape
+    L = logits.astype(np.float64)
+    mx = L.max(1)
+    lse = mx + np.log(np.exp(L - mx[:, None]).sum(1))
+    xy = L[np.arange(M), lbl]
+    loss_b = 2 * (C + 8) * U + 4 * U * (np.abs(mx) + np.abs(lse) + np.abs(xy))
+    t = np.zeros_like(L)
+    t[np.arange(M), lbl] = 1.0
+    p = d_ref.astype(np.float64) * M + t
+    d_b = (2 * (C + 8) * U * np.abs(p) + 2 * U) / M
+    return loss_b, d_b
+
+
+def check_ce(got_rows, got_d, logits, lbl, rows_ref, d_ref, d_round=0.0):
+    """CE outputs within ce_bounds (plus d_round relative for a rounded
+    gradient) and normwise rel-err 1e-5 (or d_round)."""
+    loss_b, d_b = ce_bounds(logits, lbl, d_ref)
+    if got_rows is not None:
+        err = np.abs(got_rows.astype(np.float64) - rows_ref)
+        assert np.all(err <= loss_b), f"loss rows: max excess {np.max(err - loss_b):.3e}"
+        assert np.max(err) <= 1e-5 * max(np.max(np.abs(rows_ref)), 1e-30)
+    err = np.abs(got_d.astype(np.float64) - d_ref)
+    bound = d_b + d_round * np.abs(d_ref)
+    assert np.all(err <= bound), f"dlogits: max excess {np.max(err - bound):.3e}"
+    assert np.max(err) <= max(1e-5, d_round) * np.max(np.abs(d_ref))

@@ -57,6 +57,9 @@ def test_code_objects_hold_every_dispatched_kernel():
         assert f"c3_ew_{op}_f32_v" in ew and f"c3_ew_{op}_f32_s" in ew
     red = _kernel_symbols(LIB / "reduce.hsaco")
     assert {"c3_colsum_partial_f32", "c3_colsum_final_f32", "c3_rowsum_f32"} <= red
+    loss = _kernel_symbols(LIB / "loss.hsaco")
+    assert {"c3_softmax_ce_f32", "c3_softmax_ce_bf16", "c3_cast_f32_bf16", "c3_cast_bf16_f32", "c3_sgd_f32",
+            "c3_sgd_bf16"} <= loss
 
 
 # Argument validation runs before any HIP call, so it is testable on the CPU.
@@ -92,7 +95,36 @@ def test_gemm_validation():
     assert _rc("c3hip_sum_reduce", None, 16, 4, 0, 0, None) == native.OK
 
 
+def test_train_step_helper_validation():
+    assert _rc("c3hip_softmax_ce", 5, 16, 16, 16, 16, 4, 10, None) == native.ERR_INVALID
+    assert _rc("c3hip_softmax_ce", 0, 16, 16, 16, 16, 4, 4096, None) == native.ERR_UNSUPPORTED
+    assert _rc("c3hip_softmax_ce", 0, 16, 16, 16, 16, 4, 0, None) == native.ERR_INVALID
+    assert _rc("c3hip_softmax_ce", 0, None, 16, 16, 16, 4, 10, None) == native.ERR_INVALID
+    assert _rc("c3hip_softmax_ce", 0, 16, 16, None, None, 4, 10, None) == native.OK  # nothing asked
+    assert _rc("c3hip_cast", 0, 2, 16, 16, 4, None) == native.ERR_INVALID
+    assert _rc("c3hip_cast", 0, 1, None, 16, 4, None) == native.ERR_INVALID
+    assert _rc("c3hip_cast", 0, 1, None, None, 0, None) == native.OK
+    assert _rc("c3hip_sgd_update", 0, None, 16, 0.1, 4, None) == native.ERR_INVALID
+    assert _rc("c3hip_sgd_update", 0, 16, 16, 0.1, -1, None) == native.ERR_INVALID
+
+
 def test_python_binding_raises_with_message():
     with pytest.raises(native.C3HipError) as ei:
         native.elementwise(42, native.F32, 16, 16, 0.0, 16, 4)
     assert ei.value.code == native.ERR_INVALID and "unknown elementwise op" in str(ei.value)
+
+
+def test_trainer_binding_exports_and_fails_cleanly_without_gpu():
+    from c3_amd import trainer as T
+
+    lib = T.load()
+    for name in T.SIGNATURES:
+        assert hasattr(lib, name)
+    import torch
+
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible: creation would succeed")
+    with pytest.raises(T.TrainerError, match="hipGetDevice"):
+        T.MlpTrainer([4, 2], 1)
+    with pytest.raises(T.TrainerError, match="bad arguments"):
+        T.MlpTrainer([4], 1)

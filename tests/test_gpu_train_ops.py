@@ -1,0 +1,138 @@
+"""GPU parity of the train-step helpers around the fused layers (softmax
+cross-entropy, dtype casts, SGD update) through the C ABI, against the oracle.
+
+Softmax-CE tolerance: tests/parity.py ce_bounds (exp/log within a few ulp
+on either side, a reordered row sum) plus the normwise rel-err 1e-5.  Casts
+and SGD are single roundings: bit-exact, NaN payloads aside.
+"""
+import numpy as np
+import pytest
+import torch
+
+from c3_amd import native as N
+from oracle import oracle as O
+from tests.parity import check_ce, dev, dev_bf16, empty, host, ptr
+
+pytestmark = pytest.mark.gpu
+
+U = 2.0 ** -24
+
+
+def same_bits(got, ref):
+    got = np.asarray(got, dtype=np.float32)
+    ref = np.asarray(ref, dtype=np.float32)
+    gn, rn = np.isnan(got), np.isnan(ref)
+    assert np.array_equal(gn, rn), f"NaN positions differ ({int((gn != rn).sum())})"
+    bad = got[~gn].view(np.int32) != ref[~rn].view(np.int32)
+    assert not bad.any(), f"{int(bad.sum())} elements differ, first at {np.flatnonzero(bad)[:5]}"
+
+
+def labels_dev(lbl):
+    return dev(np.ascontiguousarray(lbl, dtype=np.int32))
+
+
+@pytest.mark.parametrize("M,C", [(128, 10), (1000, 1000), (37, 65), (5, 2048), (64, 1)])
+def test_softmax_ce_f32(gpu, stream, M, C):
+    logits = O.normal(500 + C, (M, C), 0.0, 4.0)
+    lbl = O.labels(501 + C, M, C)
+    _, d_ref, rows_ref = O.softmax_ce(logits, lbl, want_rows=True)
+    dl, dlab = dev(logits), labels_dev(lbl)
+    rows, d = empty(M), empty((M, C))
+    N.softmax_ce(N.F32, ptr(dl), ptr(dlab), ptr(rows), ptr(d), M, C, stream)
+    check_ce(host(rows), host(d), logits, lbl, rows_ref, d_ref)
+    # Each output alone.
+    rows2, d2 = empty(M), empty((M, C))
+    N.softmax_ce(N.F32, ptr(dl), ptr(dlab), ptr(rows2), None, M, C, stream)
+    N.softmax_ce(N.F32, ptr(dl), ptr(dlab), None, ptr(d2), M, C, stream)
+    same_bits(host(rows2), host(rows))
+    same_bits(host(d2), host(d))
+
+
+def test_softmax_ce_closed_forms(gpu, stream):
+    # Equal logits: loss = log C, dlogits = (1/C - onehot) / M; a dominant
+    # correct logit: loss ~ 0.
+    M, C = 8, 1000
+    lbl = O.labels(510, M, C)
+    logits = np.full((M, C), -3.0, np.float32)
+    rows, d = empty(M), empty((M, C))
+    N.softmax_ce(N.F32, ptr(dev(logits)), ptr(labels_dev(lbl)), ptr(rows), ptr(d), M, C, stream)
+    assert np.allclose(host(rows), np.log(C), rtol=0, atol=2e-6)
+    exp = np.full((M, C), (1.0 / C) / M)
+    exp[np.arange(M), lbl] -= 1.0 / M
+    assert np.max(np.abs(host(d) - exp)) <= 1e-8
+    z = np.zeros((1, 10), np.float32)
+    z[0, 3] = 60.0
+    N.softmax_ce(N.F32, ptr(dev(z)), ptr(labels_dev([3])), ptr(rows), ptr(d), 1, 10, stream)
+    assert host(rows)[0] < 1e-20
+
+
+def test_softmax_ce_bad_label_gives_nan(gpu, stream):
+    M, C = 4, 10
+    logits = O.normal(520, (M, C))
+    lbl = np.array([1, -1, 10, 9], np.int32)
+    rows, d = empty(M, fill=0.0), empty((M, C), fill=0.0)
+    N.softmax_ce(N.F32, ptr(dev(logits)), ptr(labels_dev(lbl)), ptr(rows), ptr(d), M, C, stream)
+    r, g = host(rows), host(d)
+    assert np.isfinite(r[[0, 3]]).all() and np.isnan(r[[1, 2]]).all()
+    assert np.isfinite(g[[0, 3]]).all() and np.isnan(g[[1, 2]]).all()
+
+
+@pytest.mark.parametrize("M,C", [(16384 // 64, 1000), (33, 17)])
+def test_softmax_ce_bf16(gpu, stream, M, C):
+    logits = O.round_bf16(O.normal(530 + C, (M, C), 0.0, 4.0))
+    lbl = O.labels(531 + C, M, C)
+    _, d_ref, rows_ref = O.softmax_ce(logits, lbl, want_rows=True)
+    rows = empty(M)
+    d = empty((M, C), dtype=torch.bfloat16)
+    N.softmax_ce(N.BF16, ptr(dev_bf16(logits)), ptr(labels_dev(lbl)), ptr(rows), ptr(d), M, C, stream)
+    # The gradient is rounded once to bf16: half an ulp, 2^-9 relative.
+    check_ce(host(rows), host(d), logits, lbl, rows_ref, d_ref, d_round=2.0 ** -8)
+
+
+CAST_SPECIALS = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1e-40, -1e-40, 3.4e38, -3.4e38,
+                          1.0 + 2.0 ** -8, 1.0 + 3 * 2.0 ** -8, 1.0 + 2.0 ** -8 + 2.0 ** -20,
+                          3.3961e38, 9.2e-41], dtype=np.float32)
+
+
+@pytest.mark.parametrize("n", [1 << 20, 1001, 3])
+def test_cast_roundtrip(gpu, stream, n):
+    x = O.normal(540, n, 0.0, 100.0)
+    x[: min(n, len(CAST_SPECIALS))] = CAST_SPECIALS[: min(n, len(CAST_SPECIALS))]
+    bf = torch.empty(n, dtype=torch.int16, device="cuda:0")
+    back = empty(n)
+    N.cast(N.F32, N.BF16, ptr(dev(x)), ptr(bf), n, stream)
+    N.cast(N.BF16, N.F32, ptr(bf), ptr(back), n, stream)
+    torch.cuda.synchronize()
+    bits = bf.cpu().numpy().view(np.uint16)
+    ref = O.pack_bf16(x)
+    nan = np.isnan(x)
+    assert np.array_equal(bits[~nan], ref[~nan])
+    assert np.all((bits[nan] & 0x7F80) == 0x7F80) and np.all(bits[nan] & 0x7F)
+    same_bits(host(back), O.bf16_bits_to_f32(bits))
+    # Same dtype is a copy.
+    cp = empty(n)
+    N.cast(N.F32, N.F32, ptr(dev(x)), ptr(cp), n, stream)
+    same_bits(host(cp), x)
+
+
+@pytest.mark.parametrize("n", [4096 * 4096 + 3, 10])
+def test_sgd_update(gpu, stream, n):
+    w = O.normal(550, n)
+    g = O.normal(551, n)
+    sp = np.array([np.inf, -np.inf, np.nan, 0.0, -0.0, 1e-40], np.float32)
+    k = min(n, len(sp))
+    w[:k] = sp[:k]
+    g[:k] = sp[::-1][:k]
+    lr = 0.0123
+    dw = dev(w)
+    N.sgd_update(N.F32, ptr(dw), ptr(dev(g)), lr, n, stream)
+    same_bits(host(dw), O.sgd_update(w, g, lr))
+    wb = O.pack_bf16(w)
+    tb = torch.from_numpy(wb.view(np.int16).copy()).to("cuda:0")
+    N.sgd_update(N.BF16, ptr(tb), ptr(dev(g)), lr, n, stream)
+    torch.cuda.synchronize()
+    got = tb.cpu().numpy().view(np.uint16)
+    ref = O.sgd_update(wb, g, lr)
+    nan = np.isnan(O.bf16_bits_to_f32(ref))
+    assert np.array_equal(np.isnan(O.bf16_bits_to_f32(got)), nan)
+    assert np.array_equal(got[~nan], ref[~nan])

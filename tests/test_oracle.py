@@ -279,3 +279,75 @@ def test_softmax_ce_against_float64():
     p = np.exp(L - lse[:, None])
     p[np.arange(M), lbl] -= 1.0
     assert np.max(np.abs(d - p / M)) <= 1e-6
+
+
+def test_softmax_ce_closed_forms():
+    # Equal logits: every row is uniform, loss = log C, dlogits = (1/C - onehot)/M.
+    M, C = 8, 10
+    lbl = O.labels(83, M, C)
+    loss, d, rows = O.softmax_ce(np.full((M, C), 2.5, np.float32), lbl, want_rows=True)
+    assert np.allclose(rows, math.log(C), rtol=0, atol=4 * U * math.log(C) + 1e-7)
+    assert abs(loss - math.log(C)) <= 1e-6
+    exp = np.full((M, C), (1.0 / C) / M)
+    exp[np.arange(M), lbl] -= 1.0 / M
+    assert np.max(np.abs(d - exp)) <= 1e-7
+    # A dominant correct logit gives loss ~ 0 and gradient ~ 0; a dominant
+    # wrong logit gives loss ~ the margin.
+    z = np.zeros((2, 4), np.float32)
+    z[0, 1] = 50.0
+    z[1, 3] = 50.0
+    _, d, rows = O.softmax_ce(z, np.array([1, 0], np.int32), want_rows=True)
+    assert rows[0] < 1e-20 and abs(rows[1] - 50.0) < 1e-5
+    assert abs(d[0]).max() < 1e-20 and abs(d[1, 0] + 0.5) < 1e-7 and abs(d[1, 3] - 0.5) < 1e-7
+
+
+def test_softmax_ce_gradient_is_the_derivative():
+    # Central differences of the float64 mean loss along random directions
+    # agree with the oracle's dlogits; a wrong sign, a missing 1/M or a
+    # one-hot on the wrong column fails this.
+    M, C = 6, 7
+    logits = O.normal(84, (M, C), 0.0, 2.0)
+    lbl = O.labels(85, M, C)
+    _, d = O.softmax_ce(logits, lbl)
+
+    def f(L):
+        L = L.astype(np.float64)
+        m = L.max(1, keepdims=True)
+        return float(np.mean(m[:, 0] + np.log(np.exp(L - m).sum(1)) - L[np.arange(M), lbl]))
+
+    rng = np.random.default_rng(0)
+    for _ in range(5):
+        v = rng.standard_normal((M, C))
+        h = 1e-4
+        L64 = logits.astype(np.float64)
+        fd = (f(L64 + h * v) - f(L64 - h * v)) / (2 * h)
+        assert abs(fd - float(np.sum(d * v))) <= 1e-5
+    # Rows of the gradient sum to zero (softmax sums to one).
+    assert np.max(np.abs(d.sum(1))) <= 4 * C * U
+
+
+def test_softmax_ce_shift_invariance():
+    M, C = 16, 33
+    logits = O.normal(86, (M, C), 0.0, 1.0)
+    lbl = O.labels(87, M, C)
+    l0, d0, r0 = O.softmax_ce(logits, lbl, want_rows=True)
+    l1, d1, r1 = O.softmax_ce(logits + np.float32(64.0), lbl, want_rows=True)
+    # x - max is exact for both, so the softmax terms coincide up to the
+    # rounding of the shifted inputs (64 + x loses low bits of x).
+    assert np.max(np.abs(r0 - r1)) <= 64 * 2 * U * 4
+    assert np.max(np.abs(d0 - d1)) <= 1e-5
+
+
+def test_sgd_update_rounds_the_product_first():
+    lr = f32(1 + 2 ** -12)
+    g = np.array([1 + 2 ** -12], np.float32)
+    w = np.array([1 + 2 ** -11], np.float32)
+    out = O.sgd_update(w, g, float(lr))
+    step = np.float32(lr * g[0])             # rounded product
+    assert out[0] == np.float32(w[0] - step)
+    fused = np.float32(float(w[0]) - float(lr) * float(g[0]))  # single rounding
+    assert out[0] != fused
+    # bf16: 1.0 - 0.5 * 2^-8 = 1 - 2^-9 rounds (ties to even) to 1.0; 1.5 - 0.5 * 0.25 = 1.375.
+    wb = O.pack_bf16(np.array([1.0, 1.5], np.float32))
+    ob = O.sgd_update(wb, np.array([2.0 ** -8, 0.25], np.float32), 0.5)
+    assert np.array_equal(O.bf16_bits_to_f32(ob), np.array([1.0, 1.375], np.float32))
