@@ -13,6 +13,14 @@
 // stores it under the shape-mixed key, so a shape-keyed entry can only be
 // reached through find(); here the caller passes the first input's shape and
 // the lookup uses the same shape-mixed key as the install.
+//
+// Two regions with the same op sequence and the same first-input shape (two
+// Linear layers reading [M, K] with different W widths) share that key; the
+// reference keeps the last one installed and the other layer's calls fail
+// its shape check and run eagerly.  Here installWithCost also files every
+// entry under a second key that mixes all of its input shapes, and a caller
+// that passes its input shapes to matchFromPosition gets the entry compiled
+// for them (falling back to the shared key, as the reference does).
 #pragma once
 
 #include <atomic>
@@ -60,7 +68,10 @@ public:
     // Returned entries are copies (safe to use after concurrent installs).
     std::optional<RegionEntry> find(uint64_t hash);
     std::optional<RegionEntry> matchFromPosition(const std::vector<uint64_t>& prefix_hashes, size_t current_pos,
-                                                 const std::vector<size_t>& first_input_shape = {});
+                                                 const std::vector<size_t>& first_input_shape = {},
+                                                 const std::vector<std::vector<size_t>>& input_shapes = {});
+    // Key of an entry under all of its input shapes (the second index above).
+    static uint64_t variantKey(uint64_t region_key, const std::vector<std::vector<size_t>>& input_shapes);
     size_t entryCount() const;
     size_t installedCountNoLock() const { return installed_count_.load(std::memory_order_acquire); }
     bool mayMatchAsLastOp(op last_op) const {
@@ -75,6 +86,7 @@ private:
 
     mutable std::mutex mutex_;
     std::unordered_map<uint64_t, RegionEntry> entries_;
+    std::unordered_map<uint64_t, RegionEntry> variants_;  // keyed by variantKey
     std::atomic<size_t> installed_count_{0};
     static_assert(static_cast<size_t>(op::kCount) <= 64, "op::kCount exceeds the last-op bitmask");
     std::atomic<uint64_t> installed_last_ops_{0};

@@ -130,7 +130,7 @@ Tensor MlpTrainer::forward(const Tensor& X) {
         // Longest installed region starting at this layer's MatMul; only one
         // that covers exactly this layer's ops has known external inputs.
         if (regionFusionEnabled() && RF.installedCountNoLock() > 0 && RF.mayMatchAsLastOp(trace_[pos + layer_ops - 1])) {
-            auto m = RF.matchFromPosition(prefix_, pos, A.shape());
+            auto m = RF.matchFromPosition(prefix_, pos, A.shape(), {A.shape(), W_[l].shape()});
             if (m && m->len == layer_ops && m->kernel) {
                 try {
                     acts_[l + 1] = C3KernelRegistry::getInstance().executeFusedWithInputs(m->kernel, {A, W_[l], b_[l]},

@@ -276,22 +276,29 @@ C3_GEMM_BF16_KINDS(t256x128, 256, 128, 2, 2)
 C3_GEMM_BF16_KINDS(t256x256, 256, 256, 2, 2)
 
 // ===========================================================================
-// Direct-to-LDS variant (suffix _d): 256-thread blocks of 2x2 waves, each
-// wave a 128x128 sub-tile (16 MFMA blocks), 64-deep k tiles, double-buffered.
+// Direct-to-LDS kernels: 256x256 block tiles, BK-deep k tiles in STAGES LDS
+// stages, 8 waves of 128x64 (2x4) or 4 waves of 128x128 (2x2).
 // Global tiles go straight into LDS with global_load_lds_dwordx4 (lane l's
 // 16 bytes land at base + 16*l of the instruction's 1 KiB), so no staging
 // registers and no LDS stores are needed.  Layouts, per operand:
-//   KC (k contiguous in global): LDS [row][64 k], 128 B per row; the 16-byte
-//     chunk holding k 8c..8c+7 of row r sits in slot c ^ (r % 8), so the
-//     fragment reads of 8 consecutive rows hit 8 different bank groups.
-//     Fragment: one ds_read_b128 (8 consecutive k of one row).
-//   RC (row contiguous in global): LDS [64 k][ROWS], the chunk holding rows
+//   KC (k contiguous in global): LDS [row][BK k], BK/8 16-byte chunks per
+//     row; chunk c of row r sits in slot c ^ s(r), s(r) = (r >> 1) & 7 for
+//     BK = 64 and (r >> 2) & 3 for BK = 32.  Measured on MI355X (64 LDS
+//     banks): these are the XOR keys under which the 32 rows one
+//     ds_read_b128 fragment read touches fall into distinct banks; keying on
+//     r & 7 leaves a 2-way conflict.  Fragment: one ds_read_b128.
+//   RC (row contiguous in global): LDS [BK k][ROWS], the chunk holding rows
 //     8c..8c+7 of k-row kr sits in slot c ^ (2 * (kr % 4)).  Fragment: two
 //     ds_read_b64_tr_b16; in each 16-lane group lane j receives element j%4
 //     of the 8-byte pieces addressed by lanes 4r + j/4 (r = 0..3), so lanes
 //     address k-rows kbase + (j/4) at column offset 4*(j%4) and each lane
 //     gets 4 consecutive k of its own row (column).
-// Requires K % 64 == 0 and the contiguous extents % 8 == 0 (host-checked);
+// Pipeline: tiles kt+1 .. kt+STAGES-1 are in flight while tile kt is
+// multiplied.  Each wave issues the same number of DMA instructions per tile,
+// so "tile kt has landed" is s_waitcnt vmcnt(<instructions issued after it>);
+// the barrier that follows makes every wave's part of tile kt visible and
+// ends every read of the stage that is refilled next.
+// Requires K % BK == 0 and the contiguous extents % 8 == 0 (host-checked);
 // rows past M or N are loaded from a clamped address and never stored.
 // ===========================================================================
 namespace {
@@ -299,15 +306,18 @@ namespace {
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
-constexpr int kDBK = 64;
-
-template <int ROWS, bool KC, int NWAVES>
+template <int ROWS, bool KC, int NWAVES, int BK>
 struct DirectTile {
-    static constexpr int BYTES = ROWS * kDBK * 2;
+    static constexpr int BYTES = ROWS * BK * 2;
     static constexpr int NI = BYTES / 1024 / NWAVES;  // 1 KiB load instructions per wave per tile
+    static constexpr int KC_CPR = BK / 8;             // KC: 16-byte chunks per row
+    static constexpr int RC_CPR = ROWS / 8;           // RC: 16-byte chunks per k-row
     static_assert(BYTES % (1024 * NWAVES) == 0, "tile must split into whole instructions per wave");
+    static_assert(BK == 32 || BK == 64, "BK is 32 or 64");
     static_assert(KC || ROWS >= 64, "RC swizzle needs >= 8 chunks per k-row");
     uint32_t goff[NI];
+
+    __device__ __forceinline__ static int kc_key(int r) { return BK == 64 ? ((r >> 1) & 7) : ((r >> 2) & 3); }
 
     // grow0: first global row (m or n) of the tile; rows_total bounds it.
     __device__ __forceinline__ void init(int wave, int lane, int64_t ld, int64_t grow0, int64_t rows_total) {
@@ -315,15 +325,14 @@ struct DirectTile {
         for (int i = 0; i < NI; ++i) {
             const int q = wave * NI + i;
             if (KC) {
-                const int r = 8 * q + (lane >> 3);
-                const int c = (lane & 7) ^ (r & 7);
+                const int r = (64 / KC_CPR) * q + lane / KC_CPR;
+                const int c = (lane % KC_CPR) ^ kc_key(r);
                 int64_t gr = grow0 + r;
                 if (gr > rows_total - 1) gr = rows_total - 1;
                 goff[i] = (uint32_t)(gr * ld + 8 * c);
             } else {
-                constexpr int CPR = ROWS / 8;  // chunks per k-row
-                const int kr = q * (64 / CPR) + lane / CPR;
-                const int c = (lane % CPR) ^ (2 * (kr & 3));
+                const int kr = q * (64 / RC_CPR) + lane / RC_CPR;
+                const int c = (lane % RC_CPR) ^ (2 * (kr & 3));
                 int64_t gc = grow0 + 8 * c;
                 if (gc > rows_total - 8) gc = rows_total - 8;
                 goff[i] = (uint32_t)(kr * ld + gc);
@@ -334,9 +343,8 @@ struct DirectTile {
     // P advanced to the k-tile (KC: + k0, RC: + k0*ld); S = this operand's LDS tile.
     // The loads are issued through inline asm (M0 = LDS destination of the
     // instruction, wave-uniform): the compiler then does not treat them as
-    // LDS writes that every later LDS read must wait for.  The kernel orders
-    // them itself: a stage is only read after s_waitcnt vmcnt(0) and a
-    // barrier, and only refilled after the barrier that ends its last read.
+    // LDS writes that every later LDS read must wait for; the kernel orders
+    // them itself with s_waitcnt vmcnt and barriers.
     __device__ __forceinline__ void issue(const unsigned short* P, unsigned short* S, int wave) const {
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
@@ -349,12 +357,23 @@ struct DirectTile {
         }
     }
 
+    // The i-th of this wave's NI DMA instructions (same effect as issue() for
+    // that instruction alone), so the issue can be spread between MFMAs.
+    __device__ __forceinline__ void issue_one(const unsigned short* P, unsigned short* S, int wave, int i) const {
+        const uint32_t lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)(S + (wave * NI + i) * 512);
+        const unsigned short* src = P + goff[i];
+        asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+                     :
+                     : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(src)
+                     : "memory", "m0");
+    }
+
     // 8 bf16 (k = 16*st + 8*(lane/32) .. +7) of tile row r0 + lane%32.
     __device__ __forceinline__ static bf16x8 frag(const unsigned short* S, int r0, int st, int lane) {
         if (KC) {
             const int row = r0 + (lane & 31);
-            const int slot = (2 * st + (lane >> 5)) ^ (row & 7);
-            return *(const bf16x8*)(S + row * kDBK + slot * 8);
+            const int slot = (2 * st + (lane >> 5)) ^ kc_key(row);
+            return *(const bf16x8*)(S + row * BK + slot * 8);
         } else {
             const int G = lane >> 4, sp = lane & 15;
             const int col = r0 + 16 * (G & 1) + 4 * (sp & 3);
@@ -371,16 +390,35 @@ struct DirectTile {
     }
 };
 
+// s_waitcnt vmcnt(n) alone (expcnt and lgkmcnt left at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Wait until at most `after` tiles' DMA instructions (NIW per tile) are outstanding.
+template <int NIW, int PF>
+__device__ __forceinline__ void wait_tiles_after(int after) {
+    if (PF >= 4 && after >= 3) wait_vmcnt<(PF >= 4 ? 3 : 0) * NIW>();
+    else if (PF >= 3 && after >= 2) wait_vmcnt<(PF >= 3 ? 2 : 0) * NIW>();
+    else if (after >= 1) wait_vmcnt<NIW>();
+    else wait_vmcnt<0>();
+}
+
 // EPI: 0 store bf16, 1 bias + act then store bf16, 2 store fp32.
-template <int WAVES_M, int WAVES_N, bool AK, bool BKC, int EPI>
+template <int WAVES_M, int WAVES_N, bool AK, bool BKC, int EPI, int BK, int STAGES>
 __device__ __forceinline__ void gemm_bf16_direct_body(const GemmArgs& p) {
     constexpr int BM = 256, BN = 256, NW = WAVES_M * WAVES_N;
     constexpr int TM = BM / WAVES_M, TN = BN / WAVES_N, FM = TM / 32, FN = TN / 32;
-    using TA = DirectTile<BM, AK, NW>;
-    using TB = DirectTile<BN, BKC, NW>;
+    constexpr int PF = STAGES - 1;  // tiles in flight ahead of the one multiplied
+    using TA = DirectTile<BM, AK, NW, BK>;
+    using TB = DirectTile<BN, BKC, NW, BK>;
     constexpr int A_EL = TA::BYTES / 2, B_EL = TB::BYTES / 2, STAGE = A_EL + B_EL;
+    constexpr int NIW = TA::NI + TB::NI;
+    static_assert(PF * NIW < 64, "outstanding DMA instructions exceed vmcnt");
 
-    __shared__ __attribute__((aligned(1024))) unsigned short smem[2 * STAGE];
+    __shared__ __attribute__((aligned(1024))) unsigned short smem[STAGES * STAGE];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -397,8 +435,8 @@ __device__ __forceinline__ void gemm_bf16_direct_body(const GemmArgs& p) {
     TB lb;
     la.init(wave, lane, p.lda, m0, p.M);
     lb.init(wave, lane, p.ldb, n0, p.N);
-    const int64_t a_kstep = AK ? kDBK : (int64_t)kDBK * p.lda;
-    const int64_t b_kstep = BKC ? kDBK : (int64_t)kDBK * p.ldb;
+    const int64_t a_kstep = AK ? BK : (int64_t)BK * p.lda;
+    const int64_t b_kstep = BKC ? BK : (int64_t)BK * p.ldb;
 
     f32x16 acc[FM][FN];
 #pragma unroll
@@ -408,23 +446,28 @@ __device__ __forceinline__ void gemm_bf16_direct_body(const GemmArgs& p) {
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-    const int nk = (int)(p.K / kDBK);
-    la.issue(A, smem, wave);
-    lb.issue(B, smem + A_EL, wave);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+    const int nk = (int)(p.K / BK);
+#pragma unroll
+    for (int t = 0; t < PF; ++t) {
+        if (t < nk) {
+            unsigned short* S = smem + t * STAGE;
+            la.issue(A + (int64_t)t * a_kstep, S, wave);
+            lb.issue(B + (int64_t)t * b_kstep, S + A_EL, wave);
+        }
+    }
 
     for (int kt = 0; kt < nk; ++kt) {
-        const int cur = kt & 1;
-        const unsigned short* As = smem + cur * STAGE;
-        const unsigned short* Bs = As + A_EL;
-        if (kt + 1 < nk) {
-            unsigned short* Ns = smem + (cur ^ 1) * STAGE;
-            la.issue(A + (int64_t)(kt + 1) * a_kstep, Ns, wave);
-            lb.issue(B + (int64_t)(kt + 1) * b_kstep, Ns + A_EL, wave);
+        wait_tiles_after<NIW, PF>(min(nk - 1 - kt, PF - 1));
+        __syncthreads();
+        if (kt + PF < nk) {
+            unsigned short* S = smem + ((kt + PF) % STAGES) * STAGE;
+            la.issue(A + (int64_t)(kt + PF) * a_kstep, S, wave);
+            lb.issue(B + (int64_t)(kt + PF) * b_kstep, S + A_EL, wave);
         }
+        const unsigned short* As = smem + (kt % STAGES) * STAGE;
+        const unsigned short* Bs = As + A_EL;
 #pragma unroll
-        for (int st = 0; st < kDBK / 16; ++st) {
+        for (int st = 0; st < BK / 16; ++st) {
             bf16x8 af[FM], bfr[FN];
 #pragma unroll
             for (int i = 0; i < FM; ++i) af[i] = TA::frag(As, wm * TM + 32 * i, st, lane);
@@ -436,8 +479,6 @@ __device__ __forceinline__ void gemm_bf16_direct_body(const GemmArgs& p) {
                 for (int j = 0; j < FN; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
         }
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
     }
 
     const int r = lane & 31, g = lane >> 5;
@@ -467,22 +508,177 @@ __device__ __forceinline__ void gemm_bf16_direct_body(const GemmArgs& p) {
     }
 }
 
+
+// ---------------------------------------------------------------------------
+// Interleaved register-pipelined schedule (suffix _rq): 4 waves of 128x128
+// (2x2), one per SIMD, each with two fragment sets; BK-deep k tiles in STAGES
+// LDS stages, STAGES - 1 tiles in flight ahead of the one multiplied; an
+// explicit instruction order.  A wave issues in order, and a run of
+// LDS reads (or DMA issues) holds back the MFMAs queued behind it; so each
+// MFMA of step s is followed by at most one fragment read of step s + 1 and
+// one DMA instruction, and the order is pinned with scheduling barriers.
+// Measured on MI355X: issuing a k-step's 12 LDS reads as one run before its
+// 16 MFMAs costs about a third of the MFMA rate even when the MFMAs do not
+// depend on the reads.  Tile switch: at the last step, wait for the next
+// tile's DMA and pass the barrier, then interleave that step's MFMAs with
+// the next tile's first reads; the DMA of tile t + STAGES - 1 (into the stage
+// tile t - 1 used, free since the barrier that ended tile t - 1) is
+// interleaved with tile t's first-step MFMAs.
+// ---------------------------------------------------------------------------
+template <bool AK, bool BKC, int EPI, int BK, int STAGES>
+__device__ __forceinline__ void gemm_bf16_rq_body(const GemmArgs& p) {
+    constexpr int BM = 256, BN = 256, NW = 4, PF = STAGES - 1;
+    constexpr int FM = 4, FN = 4;  // 128x128 per wave
+    constexpr int KSTEPS = BK / 16;
+    using TA = DirectTile<BM, AK, NW, BK>;
+    using TB = DirectTile<BN, BKC, NW, BK>;
+    constexpr int A_EL = TA::BYTES / 2, B_EL = TB::BYTES / 2, STAGE = A_EL + B_EL;
+    constexpr int NIW = TA::NI + TB::NI;
+    static_assert(NIW <= FM * FN, "DMA instructions are spread one per MFMA");
+    static_assert(PF * NIW < 64, "outstanding DMA instructions exceed vmcnt");
+    static_assert(KSTEPS % 2 == 0, "fragment sets alternate per step");
+
+    __shared__ __attribute__((aligned(1024))) unsigned short smem[STAGES * STAGE];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+
+    int tm, tn;
+    tile_coords<8>(p.M, p.N, BM, BN, tm, tn);
+    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+
+    const unsigned short* A = (const unsigned short*)p.A;
+    const unsigned short* B = (const unsigned short*)p.B;
+    TA la;
+    TB lb;
+    la.init(wave, lane, p.lda, m0, p.M);
+    lb.init(wave, lane, p.ldb, n0, p.N);
+    const int64_t a_kstep = AK ? BK : (int64_t)BK * p.lda;
+    const int64_t b_kstep = BKC ? BK : (int64_t)BK * p.ldb;
+
+    f32x16 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+    const int nk = (int)(p.K / BK);
+    const int r0 = wm * 128, c0 = wn * 128;
+    // Tiles 0 .. PF - 1 before the loop; tile t + PF during tile t.
+#pragma unroll
+    for (int u = 0; u < PF; ++u) {
+        if (u < nk) {
+            la.issue(A + (int64_t)u * a_kstep, smem + u * STAGE, wave);
+            lb.issue(B + (int64_t)u * b_kstep, smem + u * STAGE + A_EL, wave);
+        }
+    }
+    wait_tiles_after<NIW, PF>(min(nk - 1, PF - 1));
+    __syncthreads();
+
+    bf16x8 fa[2][FM], fb[2][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i) fa[0][i] = TA::frag(smem, r0 + 32 * i, 0, lane);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) fb[0][j] = TB::frag(smem + A_EL, c0 + 32 * j, 0, lane);
+
+    for (int t = 0; t < nk; ++t) {
+        const unsigned short* As = smem + (t % STAGES) * STAGE;
+        const bool dma = t + PF < nk;
+        const unsigned short* Ag = A + (int64_t)(t + PF) * a_kstep;
+        const unsigned short* Bg = B + (int64_t)(t + PF) * b_kstep;
+        unsigned short* Sd = smem + ((t + PF) % STAGES) * STAGE;
+#pragma unroll
+        for (int s = 0; s < KSTEPS; ++s) {
+            const int cur = s & 1, nxt = cur ^ 1;
+            const bool last = s + 1 == KSTEPS;
+            const bool reads = !last || t + 1 < nk;
+            if (last && t + 1 < nk) {
+                // Tile t + 1 must have landed (tiles up to t + PF may be in flight).
+                wait_tiles_after<NIW, PF>(min(nk - 2 - t, PF - 1));
+                __builtin_amdgcn_sched_barrier(0);
+                __syncthreads();
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            const unsigned short* Sr = last ? smem + ((t + 1) % STAGES) * STAGE : As;
+            const int sr = last ? 0 : s + 1;
+#pragma unroll
+            for (int q = 0; q < FM * FN; ++q) {
+                const int i = q / FN, j = q % FN;
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cur][i], fb[cur][j], acc[i][j], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                if (reads && q < FM) fa[nxt][q] = TA::frag(Sr, r0 + 32 * q, sr, lane);
+                if (reads && q >= FM && q < FM + FN) fb[nxt][q - FM] = TB::frag(Sr + A_EL, c0 + 32 * (q - FM), sr, lane);
+                if (s == 0 && dma && q < NIW) {
+                    if (q < TA::NI)
+                        la.issue_one(Ag, Sd, wave, q);
+                    else
+                        lb.issue_one(Bg, Sd + A_EL, wave, q - TA::NI);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    }
+
+    const int r = lane & 31, g = lane >> 5;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+        const int64_t n = n0 + c0 + 32 * j + r;
+        const bool nok = n < p.N;
+        const float bv = (EPI == 1 && p.bias != nullptr && nok) ? p.bias[n] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int64_t m = m0 + r0 + 32 * i + 8 * (v >> 2) + 4 * g + (v & 3);
+                if (nok && m < p.M) {
+                    float x = acc[i][j][v];
+                    if (EPI == 1) {
+                        if (p.bias != nullptr) x = x + bv;
+                        x = act_apply(x, p.act);
+                    }
+                    if (EPI == 2)
+                        ((float*)p.C)[m * p.ldc + n] = x;
+                    else
+                        ((unsigned short*)p.C)[m * p.ldc + n] = f32_to_bf16_rne(x);
+                }
+            }
+        }
+    }
+}
+
 }  // namespace
 
-#define C3_GEMM_BF16_D(NAME, WM, WN, AK, BKC, EPI)                                          \
+#define C3_GEMM_BF16_D(NAME, WM, WN, AK, BKC, EPI, BK, ST)                                  \
     extern "C" __global__ __launch_bounds__(64 * WM * WN) void NAME(GemmArgs p) {          \
-        gemm_bf16_direct_body<WM, WN, AK, BKC, EPI>(p);                                     \
+        gemm_bf16_direct_body<WM, WN, AK, BKC, EPI, BK, ST>(p);                             \
     }
 
 // fwd: X (KC) . W (RC) + bias, act -> bf16.  dx: dZ (KC) . W^T (KC) -> bf16.
 // dw: X^T (RC) . dZ (RC) -> fp32.  dwb: same, bf16 out.  tt: A^T (RC) . B^T (KC) -> bf16.
-// d256: 4 waves of 128x128; d256w8: 8 waves of 128x64.
-#define C3_GEMM_BF16_D_KINDS(T, WM, WN)                                  \
-    C3_GEMM_BF16_D(c3_gemm_bf16_fwd_##T, WM, WN, true, false, 1)         \
-    C3_GEMM_BF16_D(c3_gemm_bf16_dx_##T, WM, WN, true, true, 0)           \
-    C3_GEMM_BF16_D(c3_gemm_bf16_dw_##T, WM, WN, false, false, 2)         \
-    C3_GEMM_BF16_D(c3_gemm_bf16_dwb_##T, WM, WN, false, false, 0)        \
-    C3_GEMM_BF16_D(c3_gemm_bf16_tt_##T, WM, WN, false, true, 0)
+#define C3_GEMM_BF16_D_KINDS(T, WM, WN, BK, ST)                                  \
+    C3_GEMM_BF16_D(c3_gemm_bf16_fwd_##T, WM, WN, true, false, 1, BK, ST)         \
+    C3_GEMM_BF16_D(c3_gemm_bf16_dx_##T, WM, WN, true, true, 0, BK, ST)           \
+    C3_GEMM_BF16_D(c3_gemm_bf16_dw_##T, WM, WN, false, false, 2, BK, ST)         \
+    C3_GEMM_BF16_D(c3_gemm_bf16_dwb_##T, WM, WN, false, false, 0, BK, ST)        \
+    C3_GEMM_BF16_D(c3_gemm_bf16_tt_##T, WM, WN, false, true, 0, BK, ST)
 
-C3_GEMM_BF16_D_KINDS(d256, 2, 2)
-C3_GEMM_BF16_D_KINDS(d256w8, 2, 4)
+// d256w8: 8 waves of 128x64, 64-deep k, 2 stages.
+C3_GEMM_BF16_D_KINDS(d256w8, 2, 4, 64, 2)
+
+
+
+#define C3_GEMM_BF16_RQ(NAME, AK, BKC, EPI, BK, ST) \
+    extern "C" __global__ __launch_bounds__(256) void NAME(GemmArgs p) { gemm_bf16_rq_body<AK, BKC, EPI, BK, ST>(p); }
+#define C3_GEMM_BF16_RQ_KINDS(T, BK, ST)                                   \
+    C3_GEMM_BF16_RQ(c3_gemm_bf16_fwd_##T, true, false, 1, BK, ST)          \
+    C3_GEMM_BF16_RQ(c3_gemm_bf16_dx_##T, true, true, 0, BK, ST)            \
+    C3_GEMM_BF16_RQ(c3_gemm_bf16_dw_##T, false, false, 2, BK, ST)          \
+    C3_GEMM_BF16_RQ(c3_gemm_bf16_dwb_##T, false, false, 0, BK, ST)         \
+    C3_GEMM_BF16_RQ(c3_gemm_bf16_tt_##T, false, true, 0, BK, ST)
+
+// d256rq: 64-deep k, 2 stages.
+C3_GEMM_BF16_RQ_KINDS(d256rq, 64, 2)

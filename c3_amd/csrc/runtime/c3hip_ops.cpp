@@ -54,6 +54,7 @@ const char* kind_name(Kind k) {
 struct Tile {
     const char* name;
     int bm, bn, threads;
+    int bk;  // k depth of one tile (direct-to-LDS kernels: K must be a multiple); 0 = any K
 };
 
 const Tile kF32Tiles[] = {{"t64x64", 64, 64, 256}, {"t128x128", 128, 128, 256}, {"t256x128", 256, 128, 512}};
@@ -68,14 +69,18 @@ const Tile* find_tile(const Tile* tiles, size_t n, const char* name) {
     return nullptr;
 }
 
-// Tile choice: the large tile once it yields at least two blocks per CU on
-// MI355X's 256 CUs, else the 64x64 tile (small layers are latency-bound).
-// C3_HIP_GEMM_TILE overrides (benchmark sweeps).
-const Tile* choose_f32_tile(int64_t M, int64_t N) {
+// fp32 tile per GEMM kind and size (C3_HIP_GEMM_TILE overrides, for sweeps).  Measured on MI355X at 8192x4096x4096:
+// the weight-gradient kinds (A read k-major, k = M = 8192 deep) run at
+// 121 TFLOP/s on 256x128 tiles against 112 on 128x128; forward and dX are
+// best on 128x128.  Small grids use 64x64 so every CU gets a block.
+const Tile* choose_f32_tile(Kind kind, int64_t M, int64_t N) {
     const size_t nt = sizeof(kF32Tiles) / sizeof(kF32Tiles[0]);
     if (const char* env = std::getenv("C3_HIP_GEMM_TILE")) {
         if (const Tile* t = find_tile(kF32Tiles, nt, env)) return t;
     }
+    const bool dw = kind == Kind::Dw || kind == Kind::DwMask;
+    const int64_t blocks256 = ((M + 255) / 256) * ((N + 127) / 128);
+    if (dw && blocks256 >= 256) return &kF32Tiles[2];
     const int64_t blocks128 = ((M + 127) / 128) * ((N + 127) / 128);
     if (blocks128 >= 512) return &kF32Tiles[1];
     return &kF32Tiles[0];
@@ -91,23 +96,26 @@ const Tile* choose_bf16_tile(int64_t M, int64_t N) {
     return &kBf16Tiles[0];
 }
 
-// Direct-to-LDS bf16 kernels (256x256 tiles, 64-deep k): plain operands
-// only (the backward masks are applied by the pre-pass), K % 64 == 0, and a
-// problem of at least 64 output tiles so the large tile fills the chip.
-const Tile kBf16Direct[] = {{"d256", 256, 256, 256}, {"d256w8", 256, 256, 512}};
+// Direct-to-LDS bf16 kernels (256x256 tiles): plain operands only (the
+// backward masks are applied by the pre-pass), K a multiple of the tile's k
+// depth, and a problem of at least 64 output tiles so the large tile fills
+// the chip.
+const Tile kBf16Direct[] = {{"d256w8", 256, 256, 512, 64}, {"d256rq", 256, 256, 256, 64}};
 
 const Tile* choose_bf16_direct(Kind kind, const GemmArgs& a) {
     if (kind == Kind::DxMask || kind == Kind::DwMask || a.db != nullptr) return nullptr;
-    if (a.K % 64 != 0 || a.K == 0) return nullptr;
+    if (a.K == 0) return nullptr;
     if (a.M < 8 || a.N < 8) return nullptr;
     const char* env = std::getenv("C3_HIP_GEMM_TILE_BF16");
     if (env) {
-        if (const Tile* t = find_tile(kBf16Direct, sizeof(kBf16Direct) / sizeof(kBf16Direct[0]), env)) return t;
+        if (const Tile* t = find_tile(kBf16Direct, sizeof(kBf16Direct) / sizeof(kBf16Direct[0]), env))
+            return a.K % t->bk == 0 ? t : nullptr;
         return nullptr;  // an explicit non-direct tile was asked for
     }
     const int64_t blocks = ((a.M + 255) / 256) * ((a.N + 255) / 256);
     if (blocks < 64) return nullptr;
-    return &kBf16Direct[1];
+    const Tile* t = &kBf16Direct[0];
+    return a.K % t->bk == 0 ? t : nullptr;
 }
 
 // bf16 kernels always move 16-byte vectors (8 elements): the contiguous
@@ -147,7 +155,7 @@ int run_gemm(int dtype, Kind kind, const GemmArgs& a0, bool a_kc, bool b_kc, hip
         void* args[] = {&a};
         return launch(name, dim3((unsigned)blocks), dim3(t->threads), args, stream);
     }
-    const Tile* t = choose_f32_tile(a.M, a.N);
+    const Tile* t = choose_f32_tile(kind, a.M, a.N);
     const bool vec = vec_ok(a_kc, a.M, a.K, a.lda, a.A, a.Amask) && vec_ok(b_kc, a.N, a.K, a.ldb, a.B, a.Bmask);
     char name[96];
     std::snprintf(name, sizeof(name), "c3_gemm_f32_%s_%s_%s", kind_name(kind), t->name, vec ? "v" : "s");

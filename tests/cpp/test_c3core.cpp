@@ -433,6 +433,21 @@ TEST(region_registry_install_and_match) {
     CHECK(!RF.matchFromPosition(p, 1, {128, 256}).has_value());  // other first-input shape
     CHECK(!RF.matchFromPosition(p, 0, {128, 784}).has_value());
     CHECK(!RF.matchFromPosition(p, 4, {128, 784}).has_value());
+    // Same op sequence and first-input shape, another W width: the shared key
+    // keeps the last install (reference behaviour), the full input shapes
+    // reach each kernel.
+    auto k2 = std::make_shared<HostKernel>(lin, 3);
+    RF.installWithCost({op::MatMul, op::Add, op::ReLU}, k2, {mn, mn, mn}, {{128, 784}, {784, 512}});
+    auto shared = RF.matchFromPosition(p, 1, {128, 784});
+    CHECK(shared.has_value() && shared->kernel == k2);
+    auto v1 = RF.matchFromPosition(p, 1, {128, 784}, {{128, 784}, {784, 256}});
+    auto v2 = RF.matchFromPosition(p, 1, {128, 784}, {{128, 784}, {784, 512}});
+    CHECK(v1.has_value() && v1->kernel == k);
+    CHECK(v2.has_value() && v2->kernel == k2);
+    auto v3 = RF.matchFromPosition(p, 1, {128, 784}, {{128, 784}, {784, 999}});  // unknown: shared key
+    CHECK(v3.has_value() && v3->kernel == k2);
+    CHECK(RegionFusionRegistry::variantKey(1, {{2, 3}}) != RegionFusionRegistry::variantKey(1, {{3, 2}}));
+    CHECK(RegionFusionRegistry::variantKey(1, {{2}, {3}}) != RegionFusionRegistry::variantKey(1, {{2, 3}}));
     // Inconsistent out_numels leave the entry inactive.
     RF.installWithCost({op::MatMul, op::Add, op::ReLU}, k, {mn, mn}, {{64, 64}, {64, 64}});
     CHECK(!RF.find(RegionFusionRegistry::regionKey(223384, {64, 64})).has_value());

@@ -177,7 +177,9 @@ def test_mlp_784_256_128_10_fp32_train_step(gpu, stream):
 
 
 def test_mlp_bf16_train_step(gpu, stream):
-    dims, batch, lr = [256, 512, 384, 100], 256, 0.05
+    # 200 classes: a multiple of 8 (bf16 vector extents) but not of 64, so the
+    # last layer's dX (inner extent 200) takes the register-staged kernels.
+    dims, batch, lr = [256, 512, 384, 200], 256, 0.05
     X, Ws, bs, lbl = make_problem(dims, batch, 0xB16, N.BF16)
     tr = T.MlpTrainer(dims, batch, N.BF16)
     tr.keep_gradients(True)

@@ -154,6 +154,24 @@ def _run_bwd(stream, X, W, Y, dY, act, want=("dX", "dW", "db")):
     return (None if dX is None else host(dX), None if dW is None else host(dW), None if db is None else host(db))
 
 
+@pytest.mark.parametrize("tile", ["t64x64", "t128x128", "t256x128"])
+@pytest.mark.parametrize("M,K,Nn", [(300, 260, 200), (257, 128, 64)])
+def test_every_fp32_tile_bit_exact(gpu, stream, monkeypatch, tile, M, K, Nn):
+    # Each tile the planner can pick, forced for every GEMM of the layer
+    # (forward, dX with mask, dW with mask and db), on ragged extents.
+    monkeypatch.setenv("C3_HIP_GEMM_TILE", tile)
+    X, W, Y, dY = _bwd_inputs(61, M, K, Nn, True)
+    b = ints(64, Nn)
+    Yg = empty((M, Nn))
+    N.linear_fwd(N.F32, ptr(dev(X)), ptr(dev(W)), ptr(dev(b)), ptr(Yg), M, K, Nn, 1, stream)
+    same_bits(host(Yg), O.linear_fwd(X, W, b, 1))
+    gX, gW, gb = _run_bwd(stream, X, W, Y, dY, 1)
+    rX, rW, rb = O.linear_bwd(X, W, Y, dY, 1)
+    same_bits(gX, rX)
+    same_bits(gW, rW)
+    same_bits(gb, rb)
+
+
 @pytest.mark.parametrize("M,K,Nn", BWD_SHAPES)
 @pytest.mark.parametrize("act", [1, 0])
 def test_linear_bwd_integer_bit_exact(gpu, stream, M, K, Nn, act):
@@ -265,6 +283,29 @@ def test_bf16_integer_bit_exact(gpu, stream, M, K, Nn, act):
     N.linear_bwd(N.BF16, ptr(dev_bf16(X)), ptr(dev_bf16(W)), ptr(Y), ptr(dev_bf16(dY)), ptr(dX), ptr(dW), ptr(db),
                  M, K, Nn, act, stream)
     rX, rW, rb = O.linear_bwd(X, W, rY, dY, act)
+    same_bits(host(dX), _bf16_round(rX))
+    same_bits(host(dW), rW)
+    same_bits(host(db), rb)
+
+
+@pytest.mark.parametrize("tile", ["d256w8", "d256rq", "t64x64", "t128x128", "t256x128", "t256x256"])
+def test_every_bf16_tile_bit_exact(gpu, stream, monkeypatch, tile):
+    # Each bf16 kernel family forced for the forward and every backward GEMM,
+    # on ragged M and N (the 256x256 tiles run 2x2 blocks with partial edges).
+    from tests.parity import dev_bf16
+
+    monkeypatch.setenv("C3_HIP_GEMM_TILE_BF16", tile)
+    M, K, Nn = 320, 256, 264
+    X, W, b, dY = ints(85, (M, K)), ints(86, (K, Nn)), ints(87, Nn), ints(88, (M, Nn))
+    Y = empty((M, Nn), dtype=torch.bfloat16)
+    N.linear_fwd(N.BF16, ptr(dev_bf16(X)), ptr(dev_bf16(W)), ptr(dev(b)), ptr(Y), M, K, Nn, 1, stream)
+    rY = _bf16_round(O.linear_fwd(X, W, b, 1))
+    same_bits(host(Y), rY)
+    dX = empty((M, K), dtype=torch.bfloat16)
+    dW, db = empty((K, Nn)), empty(Nn)
+    N.linear_bwd(N.BF16, ptr(dev_bf16(X)), ptr(dev_bf16(W)), ptr(Y), ptr(dev_bf16(dY)), ptr(dX), ptr(dW), ptr(db),
+                 M, K, Nn, 1, stream)
+    rX, rW, rb = O.linear_bwd(X, W, rY, dY, 1)
     same_bits(host(dX), _bf16_round(rX))
     same_bits(host(dW), rW)
     same_bits(host(db), rb)
