@@ -12,15 +12,24 @@
 //                bias row (SumReduce axis 0)      []      (:618-644, :1641-1700)
 //   MatMul in:0  grad . B^T                       [B]     (:681-708)
 //          in:1  A^T . grad                       [A]     (:709-723)
+//   Sigmoid in:0 s = 1/(1+exp(-x)); grad*(s*(1-s)) [x]    (:530-567)
+//   Tanh   in:0  t via exp; grad * (1 - t*t)      [x]     (:569-616)
+//   Exp    in:0  exp(x) * grad                    [x]     (:823-849)
+//   Log    in:0  grad / x                         [x]     (:851-872)
+//   Neg    in:0  -grad                            []      (:725-741)
+//   Sub    in:0  grad; in:1 -grad                 []      (:743-770)
+//   Mul    in:0  grad * B [B]; in:1 A * grad [A]  (buildMulBackwardGraph)
+//   Div    in:0  grad / B [B]; in:1 -((A/(B*B))*grad) [A, B] (buildDivBackwardGraph)
+// Mul/Sub/Div with broadcast operands are not compiled (the host runs eager).
 // The reference never compiles Add's identity input (so Add backward, db
 // included, always falls back to eager) and respawns a compile on every
 // miss; here the identity is an installed no-copy kernel and a key is
 // compiled at most once at a time.  The node type is passed as a string
 // (the host framework's autograd Node is not part of this build).
 //
-// tryExecuteLinearBackward is the fused backward of a whole
-// MatMul+Add(+ReLU) layer -- ReLU mask, dX, dW and db in the two GEMM
-// launches of c3hip_linear_bwd -- keyed "Linear[+ReLU]|grad:...|inputs:...|fused".
+// tryExecuteLinearBackward is the fused backward of a whole MatMul+Add(+act)
+// layer -- the activation's derivative from Y, dX, dW and db in
+// c3hip_linear_bwd -- keyed "Linear[+ReLU|+Sigmoid|+Tanh]|grad:...|inputs:...|fused".
 #pragma once
 
 #include <atomic>
@@ -46,9 +55,14 @@ public:
 
     std::optional<std::vector<Tensor>> tryExecuteBackward(const std::string& node_type, const Tensor& grad,
                                                           const std::vector<Tensor>& forward_inputs);
-    // forward_inputs = {X, W, Y}; returns {dX, dW, db}.  relu: the layer ends in ReLU.
+    // forward_inputs = {X, W, Y}; returns {dX, dW, db}.  act: C3HIP_ACT_* of
+    // the layer (relu = true is C3HIP_ACT_RELU, false no activation).
     std::optional<std::vector<Tensor>> tryExecuteLinearBackward(const Tensor& grad,
-                                                                const std::vector<Tensor>& forward_inputs, bool relu);
+                                                                const std::vector<Tensor>& forward_inputs, int act);
+    std::optional<std::vector<Tensor>> tryExecuteLinearBackward(const Tensor& grad,
+                                                                const std::vector<Tensor>& forward_inputs, bool relu) {
+        return tryExecuteLinearBackward(grad, forward_inputs, relu ? 1 : 0);
+    }
 
     static bool supportsNodeType(const std::string& node_type);
     static std::string makeBaseKey(const std::string& node_type, const Tensor& grad,

@@ -63,10 +63,13 @@ struct CompileOptions {
 
 // What a compile produces: one kernel family entry of the C ABI.
 enum class KernelKind {
-    Elementwise,   // single-node add/sub/mul/div/relu/neg/scale (+ relu-bwd mask-mul)
+    Elementwise,   // single-node add/sub/mul/div/relu/neg/scale/sigmoid/tanh/exp/log (+ relu-bwd mask-mul),
+                   // inputs in operand order
     MatMul,        // single-node c3.matmul with transA/transB
-    LinearFwd,     // region MatMul+Add(+ReLU): inputs [X, W, b]
+    LinearFwd,     // region MatMul(+Add)(+act): inputs [X, W(, b)]
     ReLUBackward,  // ReLU node backward: inputs [grad, x] -> (x > 0 ? 1 : 0) * grad
+    UnaryBackward, // Sigmoid/Tanh/Exp node backward: inputs [grad, x] -> ew_op(x, grad)
+    DivBackwardB,  // Div node backward, input 1: inputs [grad, A, B] -> -((A / (B*B)) * grad)
     AddBackwardLhs,// Add node backward, input 0: identity on grad
     SumReduce,     // Add node backward, input 1 (bias): column sums of grad
     MatMulBackwardA, // MatMul node backward, input 0: grad . B^T, inputs [grad, B]

@@ -15,7 +15,10 @@ C3BackwardCapture& C3BackwardCapture::getInstance() {
     return c;
 }
 
-bool C3BackwardCapture::supportsNodeType(const std::string& t) { return t == "ReLU" || t == "Add" || t == "MatMul"; }
+bool C3BackwardCapture::supportsNodeType(const std::string& t) {
+    return t == "ReLU" || t == "Add" || t == "MatMul" || t == "Sigmoid" || t == "Tanh" || t == "Exp" || t == "Log" ||
+           t == "Neg" || t == "Sub" || t == "Mul" || t == "Div";
+}
 
 bool C3BackwardCapture::deviceSupported(DeviceType dev) const {
     return dev == DeviceType::kHIP || C3Engine::getInstance().hasFactoryForTest();
@@ -78,6 +81,62 @@ bool C3BackwardCapture::buildBackwardSpecForInput(const std::string& node_type, 
             return false;
         }
         *num_inputs = 2;
+    } else if (node_type == "Sigmoid" || node_type == "Tanh" || node_type == "Exp") {
+        // [grad, x] -> f'(x) * grad with the reference's graph (x = forward_inputs[0]).
+        if (i != 0 || in.size() != 1 || in[0] != g || dt != DType::kFloat) return false;
+        s.kind = KernelKind::UnaryBackward;
+        s.op_seq = {node_type == "Sigmoid" ? op::Sigmoid : node_type == "Tanh" ? op::Tanh : op::Exp};
+        s.ew_op = node_type == "Sigmoid" ? C3HIP_EW_SIGMOID_BWD : node_type == "Tanh" ? C3HIP_EW_TANH_BWD : C3HIP_EW_EXP_BWD;
+        s.input_shapes = {g, in[0]};
+        s.out_shape = g;
+        *map = {0};
+        *num_inputs = 2;
+    } else if (node_type == "Log") {
+        // grad / x  [grad, x]  (buildLogBackwardGraph)
+        if (i != 0 || in.size() != 1 || in[0] != g || dt != DType::kFloat) return false;
+        s.kind = KernelKind::Elementwise;
+        s.op_seq = {op::Log};
+        s.ew_op = C3HIP_EW_DIV;
+        s.input_shapes = {g, in[0]};
+        s.out_shape = g;
+        *map = {0};
+        *num_inputs = 2;
+    } else if (node_type == "Neg" || node_type == "Sub") {
+        // Neg: -grad; Sub: in:0 grad, in:1 -grad  [grad]  (buildNegBackwardGraph, buildSubBackwardGraph)
+        if (dt != DType::kFloat) return false;
+        if (node_type == "Neg" ? (i != 0 || in.size() != 1 || in[0] != g)
+                               : (in.size() != 2 || i >= 2 || in[i] != g))
+            return false;
+        s.op_seq = {node_type == "Neg" ? op::Neg : op::Sub};
+        s.input_shapes = {g};
+        s.out_shape = g;
+        *num_inputs = 1;
+        if (node_type == "Sub" && i == 0) {
+            s.kind = KernelKind::AddBackwardLhs;
+        } else {
+            s.kind = KernelKind::Elementwise;
+            s.ew_op = C3HIP_EW_NEG;
+        }
+    } else if (node_type == "Mul" || node_type == "Div") {
+        // Mul: in:0 grad * B [grad, B], in:1 A * grad [grad, A]; Div: in:0 grad / B [grad, B],
+        // in:1 -((A / (B*B)) * grad) [grad, A, B]  (buildMulBackwardGraph, buildDivBackwardGraph).
+        // Broadcast operands would need a reduction: not compiled (eager).
+        if (in.size() != 2 || i >= 2 || in[0] != g || in[1] != g || dt != DType::kFloat) return false;
+        const bool div = node_type == "Div";
+        s.op_seq = {div ? op::Div : op::Mul};
+        s.out_shape = g;
+        if (div && i == 1) {
+            s.kind = KernelKind::DivBackwardB;
+            s.input_shapes = {g, in[0], in[1]};
+            *map = {0, 1};
+            *num_inputs = 3;
+        } else {
+            s.kind = KernelKind::Elementwise;
+            s.ew_op = div ? C3HIP_EW_DIV : C3HIP_EW_MUL;
+            s.input_shapes = {g, in[1 - i]};
+            *map = {1 - i};
+            *num_inputs = 2;
+        }
     } else {
         return false;
     }
@@ -149,13 +208,18 @@ std::optional<std::vector<Tensor>> C3BackwardCapture::tryExecuteBackward(const s
 
 std::optional<std::vector<Tensor>> C3BackwardCapture::tryExecuteLinearBackward(const Tensor& grad,
                                                                                const std::vector<Tensor>& fwd,
-                                                                               bool relu) {
+                                                                               int act) {
     if (!backwardFusionEnabled()) return std::nullopt;
     if (fwd.size() != 3 || !deviceSupported(grad.device())) {
         unsupported_++;
         return std::nullopt;
     }
-    const std::string key = makeBaseKey(relu ? "Linear+ReLU" : "Linear", grad, fwd) + "|fused";
+    if (act < C3HIP_ACT_NONE || act > C3HIP_ACT_TANH) {
+        unsupported_++;
+        return std::nullopt;
+    }
+    static const char* const kNames[] = {"Linear", "Linear+ReLU", "Linear+Sigmoid", "Linear+Tanh"};
+    const std::string key = makeBaseKey(kNames[act], grad, fwd) + "|fused";
     // Graph inputs [dY, X, W, Y]: forward_inputs {X, W, Y} in order.
     auto r = C3KernelRegistry::getInstance().tryExecuteBackward(key, grad, fwd);
     if (r && r->size() == 3) {
@@ -170,8 +234,11 @@ std::optional<std::vector<Tensor>> C3BackwardCapture::tryExecuteLinearBackward(c
     }
     KernelSpec s;
     s.kind = KernelKind::LinearBwd;
-    s.op_seq = relu ? std::vector<op>{op::MatMul, op::Add, op::ReLU} : std::vector<op>{op::MatMul, op::Add};
-    s.act = relu ? C3HIP_ACT_RELU : C3HIP_ACT_NONE;
+    s.op_seq = {op::MatMul, op::Add};
+    if (act == C3HIP_ACT_RELU) s.op_seq.push_back(op::ReLU);
+    if (act == C3HIP_ACT_SIGMOID) s.op_seq.push_back(op::Sigmoid);
+    if (act == C3HIP_ACT_TANH) s.op_seq.push_back(op::Tanh);
+    s.act = act;
     s.dtype = X.dtype();
     s.input_shapes = {grad.shape(), X.shape(), W.shape(), fwd[2].shape()};
     s.out_shape = X.shape();

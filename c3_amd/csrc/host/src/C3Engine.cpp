@@ -21,6 +21,8 @@ const char* kindName(KernelKind k) {
         case KernelKind::MatMul: return "matmul";
         case KernelKind::LinearFwd: return "linear_fwd";
         case KernelKind::ReLUBackward: return "relu_bwd";
+        case KernelKind::UnaryBackward: return "unary_bwd";
+        case KernelKind::DivBackwardB: return "div_bwd_b";
         case KernelKind::AddBackwardLhs: return "add_bwd_lhs";
         case KernelKind::SumReduce: return "sum_reduce";
         case KernelKind::MatMulBackwardA: return "matmul_bwd_a";
@@ -78,7 +80,9 @@ std::string KernelSpec::toString() const {
 std::string KernelSpec::moduleName() const {
     switch (kind) {
         case KernelKind::Elementwise:
-        case KernelKind::ReLUBackward: return "elementwise";
+        case KernelKind::ReLUBackward:
+        case KernelKind::UnaryBackward:
+        case KernelKind::DivBackwardB: return "elementwise";
         case KernelKind::SumReduce: return "reduce";
         case KernelKind::AddBackwardLhs: return "";
         default: return dtype == DType::kBFloat16 ? "gemm_bf16" : "gemm_f32";

@@ -66,7 +66,7 @@ size_t C3HotPathManager::hashShapeKey(const std::vector<size_t>& shape, op op_ty
 bool C3HotPathManager::isSupportedOp(op op_type) {
     switch (op_type) {
         case op::Add: case op::Sub: case op::Mul: case op::Div: case op::MatMul: case op::Neg: case op::ReLU:
-        case op::Tanh: case op::Sigmoid:
+        case op::Tanh: case op::Sigmoid: case op::Exp: case op::Log:
             return true;
         default:
             return false;
@@ -85,6 +85,10 @@ bool C3HotPathManager::buildSingleOpSpec(op op_type, const std::vector<size_t>& 
         case op::Div: s.ew_op = C3HIP_EW_DIV; break;
         case op::Neg: s.ew_op = C3HIP_EW_NEG; break;
         case op::ReLU: s.ew_op = C3HIP_EW_RELU; break;
+        case op::Sigmoid: s.ew_op = C3HIP_EW_SIGMOID; break;
+        case op::Tanh: s.ew_op = C3HIP_EW_TANH; break;
+        case op::Exp: s.ew_op = C3HIP_EW_EXP; break;
+        case op::Log: s.ew_op = C3HIP_EW_LOG; break;
         case op::MatMul: {
             if (lhs.size() != 2 || rhs.size() != 2 || lhs[1] != rhs[0]) return false;
             s.kind = KernelKind::MatMul;
@@ -94,12 +98,14 @@ bool C3HotPathManager::buildSingleOpSpec(op op_type, const std::vector<size_t>& 
             return true;
         }
         default:
-            return false;  // Tanh / Sigmoid: no gfx950 kernel in this build
+            return false;
     }
     if (dt != DType::kFloat) return false;
     s.kind = KernelKind::Elementwise;
     s.input_shapes = {lhs};
-    if (op_type != op::Neg && op_type != op::ReLU) s.input_shapes.push_back(rhs);
+    const bool unary = op_type == op::Neg || op_type == op::ReLU || op_type == op::Sigmoid || op_type == op::Tanh ||
+                       op_type == op::Exp || op_type == op::Log;
+    if (!unary) s.input_shapes.push_back(rhs);
     s.out_shape = lhs;
     *out = s;
     return true;
@@ -114,16 +120,16 @@ bool C3HotPathManager::buildFusedSpec(const std::vector<DispatchRecord>& recs, c
     s.dtype = recs[0].dtype;
     s.out_shape = {M, N};
     for (const auto& r : recs) s.op_seq.push_back(r.op_type);
-    if (pattern == "MatMul+Add+ReLU") {
+    if (pattern == "MatMul+Add+ReLU" || pattern == "MatMul+Add+Sigmoid") {
         // The fused kernel adds a per-column bias row: the Add's rhs must hold N values.
         if (recs.size() != 3 || numelOf(recs[1].rhs_shape) != N) return false;
-        s.act = C3HIP_ACT_RELU;
+        s.act = pattern == "MatMul+Add+ReLU" ? C3HIP_ACT_RELU : C3HIP_ACT_SIGMOID;
         s.input_shapes = {{M, K}, {K, N}, {N}};
-    } else if (pattern == "MatMul+ReLU") {
-        s.act = C3HIP_ACT_RELU;
-        s.input_shapes = {{M, K}, {K, N}};
+    } else if (pattern == "MatMul+ReLU" || pattern == "MatMul+Sigmoid") {
+        s.act = pattern == "MatMul+ReLU" ? C3HIP_ACT_RELU : C3HIP_ACT_SIGMOID;
+        s.input_shapes = {{M, K}, {K, N}};  // no bias
     } else {
-        return false;  // Sigmoid epilogues have no gfx950 kernel in this build
+        return false;
     }
     *out = s;
     return true;

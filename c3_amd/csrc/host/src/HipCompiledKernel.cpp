@@ -63,7 +63,9 @@ std::vector<Tensor> HipCompiledKernel::execute(const std::vector<Tensor>& in) {
     switch (s.kind) {
         case KernelKind::Elementwise: {
             const bool binary = s.ew_op == C3HIP_EW_ADD || s.ew_op == C3HIP_EW_SUB || s.ew_op == C3HIP_EW_MUL ||
-                                s.ew_op == C3HIP_EW_DIV || s.ew_op == C3HIP_EW_RELU_BWD;
+                                s.ew_op == C3HIP_EW_DIV || s.ew_op == C3HIP_EW_RELU_BWD ||
+                                s.ew_op == C3HIP_EW_SIGMOID_BWD || s.ew_op == C3HIP_EW_TANH_BWD ||
+                                s.ew_op == C3HIP_EW_EXP_BWD;
             need(binary ? 2 : 1);
             const Tensor& a = in[0];
             if (a.dtype() != DType::kFloat) throw std::runtime_error("elementwise ops take fp32");
@@ -100,14 +102,16 @@ std::vector<Tensor> HipCompiledKernel::execute(const std::vector<Tensor>& in) {
             return {C};
         }
         case KernelKind::LinearFwd: {
-            need(3);
-            const Tensor &X = in[0], &W = in[1], &b = in[2];
+            // [X, W, b] for MatMul+Add+act, [X, W] for MatMul+act.
+            const bool has_bias = s.input_shapes.size() != 2;
+            need(has_bias ? 3 : 2);
+            const Tensor &X = in[0], &W = in[1];
             const size_t M = X.shape()[0], K = X.shape()[1], N = W.shape()[1];
-            if (W.shape()[0] != K || b.numel() != N || b.dtype() != DType::kFloat)
+            if (W.shape()[0] != K || (has_bias && (in[2].numel() != N || in[2].dtype() != DType::kFloat)))
                 throw std::runtime_error("linear: shapes of X, W, b do not agree");
             Tensor Y(ShapeTag{}, {M, N}, X.dtype(), DeviceType::kHIP);
-            check(c3hip_linear_fwd(hipDtype(X.dtype()), X.data(), W.data(), b.data_ptr<float>(), Y.data(), (int64_t)M,
-                                   (int64_t)K, (int64_t)N, s.act, st),
+            check(c3hip_linear_fwd(hipDtype(X.dtype()), X.data(), W.data(), has_bias ? in[2].data_ptr<float>() : nullptr,
+                                   Y.data(), (int64_t)M, (int64_t)K, (int64_t)N, s.act, st),
                   "c3hip_linear_fwd");
             return {Y};
         }
@@ -120,6 +124,28 @@ std::vector<Tensor> HipCompiledKernel::execute(const std::vector<Tensor>& in) {
             check(c3hip_elementwise(C3HIP_EW_RELU_BWD, C3HIP_F32, x.data(), g.data(), 0.0f, out.data(),
                                     (int64_t)g.numel(), 0, st),
                   "c3hip_elementwise(relu_bwd)");
+            return {out};
+        }
+        case KernelKind::UnaryBackward: {
+            need(2);  // [grad, x] -> ew_op(x, grad)
+            const Tensor &g = in[0], &x = in[1];
+            if (g.shape() != x.shape() || g.dtype() != DType::kFloat || x.dtype() != DType::kFloat)
+                throw std::runtime_error("unary backward: grad and input differ in shape or are not fp32");
+            Tensor out(ShapeTag{}, g.shape(), DType::kFloat, DeviceType::kHIP);
+            check(c3hip_elementwise(s.ew_op, C3HIP_F32, x.data(), g.data(), 0.0f, out.data(), (int64_t)g.numel(), 0, st),
+                  "c3hip_elementwise(backward)");
+            return {out};
+        }
+        case KernelKind::DivBackwardB: {
+            need(3);  // [grad, A, B] -> -((A / (B*B)) * grad)
+            const Tensor &g = in[0], &a = in[1], &b = in[2];
+            if (g.shape() != a.shape() || g.shape() != b.shape() || g.dtype() != DType::kFloat ||
+                a.dtype() != DType::kFloat || b.dtype() != DType::kFloat)
+                throw std::runtime_error("div backward: operands differ in shape or are not fp32");
+            Tensor out(ShapeTag{}, g.shape(), DType::kFloat, DeviceType::kHIP);
+            check(c3hip_elementwise3(C3HIP_EW3_DIV_BWD_B, C3HIP_F32, a.data(), b.data(), g.data(), out.data(),
+                                     (int64_t)g.numel(), st),
+                  "c3hip_elementwise3");
             return {out};
         }
         case KernelKind::AddBackwardLhs: {

@@ -9,6 +9,15 @@
 //                     src/C3/LinalgElementwiseGen.cpp:168-186)
 //   relu_bwd        : Gt(z, 0) then Mul(mask, grad),
 //                     src/C3/C3BackwardCapture.cpp:501-528 + src/C3/MLIRKernelGen.cpp:173-211
+//   sigmoid         : 1 / (1 + exp(-x)), SigmoidOpLowering, src/C3/C3DialectLowering.cpp:352-380
+//   tanh, exp, log  : math.tanh / math.exp / math.log, UnaryOpLowering :321-323
+//   sigmoid_bwd     : s = 1/(1+exp(-x)); grad * (s * (1 - s)), src/C3/C3BackwardCapture.cpp:530-567
+//   tanh_bwd        : t = (e^x - e^-x) / (e^x + e^-x); grad * (1 - t*t), :569-616 (the
+//                     reference recomputes tanh through exp here, so |x| > ~88.7 gives
+//                     inf/inf = NaN; kept)
+//   exp_bwd         : exp(x) * grad, :823-849
+//   div_bwd_b (3-in): -((a / (b*b)) * grad), buildDivBackwardGraph
+// exp, log and tanh are the device library's expf, logf, tanhf.
 //
 // Layout: flat contiguous fp32 arrays.  Fast path: one 16-byte vector per
 // operand per thread and a block per 256 vectors, non-temporal hints (the
@@ -21,10 +30,16 @@
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-enum { EW_ADD = 0, EW_SUB = 1, EW_MUL = 2, EW_DIV = 3, EW_RELU = 4, EW_RELU_BWD = 5, EW_NEG = 6, EW_SCALE = 7 };
+enum {
+    EW_ADD = 0, EW_SUB = 1, EW_MUL = 2, EW_DIV = 3, EW_RELU = 4, EW_RELU_BWD = 5, EW_NEG = 6, EW_SCALE = 7,
+    EW_SIGMOID = 8, EW_TANH = 9, EW_EXP = 10, EW_LOG = 11, EW_SIGMOID_BWD = 12, EW_TANH_BWD = 13, EW_EXP_BWD = 14
+};
 
+// Each step below is one IEEE operation of the reference's graph, rounded to
+// fp32 in the same order (no multiply-add contraction: see the pragma).
 template <int OP>
 __device__ __forceinline__ float ew_apply(float a, float b, float alpha) {
+#pragma clang fp contract(off)
     if (OP == EW_ADD) return a + b;
     if (OP == EW_SUB) return a - b;
     if (OP == EW_MUL) return a * b;
@@ -32,12 +47,29 @@ __device__ __forceinline__ float ew_apply(float a, float b, float alpha) {
     if (OP == EW_RELU) return fmaxf(a, 0.0f);    // maxnum: NaN -> 0
     if (OP == EW_RELU_BWD) return (a > 0.0f ? 1.0f : 0.0f) * b;
     if (OP == EW_NEG) return -a;
+    if (OP == EW_SIGMOID) return 1.0f / (1.0f + expf(-a));
+    if (OP == EW_TANH) return tanhf(a);
+    if (OP == EW_EXP) return expf(a);
+    if (OP == EW_LOG) return logf(a);
+    if (OP == EW_SIGMOID_BWD) {
+        const float s = 1.0f / (1.0f + expf(-a));
+        const float t = s * (1.0f - s);
+        return b * t;
+    }
+    if (OP == EW_TANH_BWD) {
+        const float e = expf(a), en = expf(-a);
+        const float t = (e - en) / (e + en);
+        const float sq = t * t;
+        return b * (1.0f - sq);
+    }
+    if (OP == EW_EXP_BWD) return expf(a) * b;
     return a * alpha;                            // EW_SCALE
 }
 
 template <int OP>
 constexpr bool ew_binary() {
-    return OP == EW_ADD || OP == EW_SUB || OP == EW_MUL || OP == EW_DIV || OP == EW_RELU_BWD;
+    return OP == EW_ADD || OP == EW_SUB || OP == EW_MUL || OP == EW_DIV || OP == EW_RELU_BWD ||
+           OP == EW_SIGMOID_BWD || OP == EW_TANH_BWD || OP == EW_EXP_BWD;
 }
 
 constexpr int kThreads = 256;
@@ -105,3 +137,25 @@ C3_EW(relu, EW_RELU)
 C3_EW(relu_bwd, EW_RELU_BWD)
 C3_EW(neg, EW_NEG)
 C3_EW(scale, EW_SCALE)
+C3_EW(sigmoid, EW_SIGMOID)
+C3_EW(tanh, EW_TANH)
+C3_EW(exp, EW_EXP)
+C3_EW(log, EW_LOG)
+C3_EW(sigmoid_bwd, EW_SIGMOID_BWD)
+C3_EW(tanh_bwd, EW_TANH_BWD)
+C3_EW(exp_bwd, EW_EXP_BWD)
+
+// Three-input ops: out = op(a, b, c), no broadcast, any n and alignment.
+extern "C" __global__ __launch_bounds__(kThreads) void c3_ew3_div_bwd_b_f32(const float* __restrict__ a,
+                                                                          const float* __restrict__ b,
+                                                                          const float* __restrict__ c,
+                                                                          float* __restrict__ out, int64_t n) {
+#pragma clang fp contract(off)
+    const int64_t stride = (int64_t)gridDim.x * kThreads;
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += stride) {
+        const float bb = b[i] * b[i];
+        const float q = a[i] / bb;
+        const float m = q * c[i];
+        out[i] = -m;
+    }
+}

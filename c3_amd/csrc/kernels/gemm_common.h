@@ -56,8 +56,14 @@ __device__ __forceinline__ void tile_coords(int64_t M, int64_t N, int BM, int BN
 
 __device__ __forceinline__ float relu_mask(float y) { return y > 0.0f ? 1.0f : 0.0f; }
 
-// maxnum(x, 0): NaN -> 0 (llvm.maxnum semantics, v_max_f32).
-__device__ __forceinline__ float act_apply(float v, int act) { return act == 1 ? fmaxf(v, 0.0f) : v; }
+// act 1: maxnum(x, 0) (NaN -> 0, llvm.maxnum semantics, v_max_f32);
+// act 2: 1 / (1 + expf(-x)); act 3: tanhf(x) (device library expf/tanhf).
+__device__ __forceinline__ float act_apply(float v, int act) {
+    if (act == 1) return fmaxf(v, 0.0f);
+    if (act == 2) return 1.0f / (1.0f + expf(-v));
+    if (act == 3) return tanhf(v);
+    return v;
+}
 
 __device__ __forceinline__ unsigned short f32_to_bf16_rne(float x) {
     uint32_t u = __float_as_uint(x);

@@ -72,18 +72,57 @@ extern "C" __global__ __launch_bounds__(kThreads) void c3_rowsum_f32(
     if (lane == 0) out[row] = s;
 }
 
-// ---- bf16 backward pre-pass ----------------------------------------------
-// dZ = (Y > 0 ? 1 : 0) * dY on bf16 [M, N] (relu != 0; else dZ = dY), written
-// to dZ when non-null, and per-chunk column sums of dZ in fp32 into part
-// [nchunks, N] when non-null (the bias gradient, finished by
-// c3_colsum_final_f32).  One thread owns 8 consecutive columns (a 16-byte
-// vector) of a chunk of rows; consecutive threads cover consecutive vectors
-// of a row.  Requires N % 8 == 0 and 16-byte aligned rows.
+// ---- backward pre-passes ---------------------------------------------------
+// dZ = act'(Y) * dY, the gradient at the pre-activation, from the layer's
+// output Y (act 1: (Y > 0 ? 1 : 0) * dY; act 2: dY * (Y * (1 - Y)); act 3:
+// dY * (1 - Y * Y); act 0: dY), written to dZ when non-null, and per-chunk
+// column sums of dZ in fp32 into part [nchunks, N] when non-null (the bias
+// gradient, finished by c3_colsum_final_f32).  Each step is one IEEE
+// operation in the order written (no multiply-add contraction).
 #include "gemm_common.h"
 
+__device__ __forceinline__ float act_grad(float y, float d, int act) {
+#pragma clang fp contract(off)
+    if (act == 1) return (y > 0.0f ? 1.0f : 0.0f) * d;
+    if (act == 2) {
+        const float t = y * (1.0f - y);
+        return d * t;
+    }
+    if (act == 3) {
+        const float sq = y * y;
+        return d * (1.0f - sq);
+    }
+    return d;
+}
+
+// fp32: one thread per column of a chunk of rows (consecutive threads read
+// consecutive columns of a row).
+extern "C" __global__ __launch_bounds__(kThreads) void c3_dz_colsum_f32(
+    const float* __restrict__ Y, const float* __restrict__ dY, float* __restrict__ dZ, float* __restrict__ part,
+    int64_t M, int64_t N, int64_t rows_per_chunk, int act) {
+    const int64_t n = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (n >= N) return;
+    const int64_t chunk = blockIdx.y;
+    const int64_t r0 = chunk * rows_per_chunk;
+    const int64_t r1 = min(M, r0 + rows_per_chunk);
+    float s = 0.0f;
+    for (int64_t i = r0; i < r1; ++i) {
+        const int64_t off = i * N + n;
+        const float d = act_grad(act ? Y[off] : 0.0f, dY[off], act);
+        if (dZ) dZ[off] = d;
+        s += d;
+    }
+    if (part) part[chunk * N + n] = s;
+}
+
+// bf16: one thread owns 8 consecutive columns (a 16-byte vector) of a chunk
+// of rows; consecutive threads cover consecutive vectors of a row.  ReLU
+// works on the bit patterns (exact); sigmoid and tanh compute in fp32 and
+// round dZ to bf16 once (nearest even); the column sums add the rounded
+// values the GEMMs then read.  Requires N % 8 == 0 and 16-byte aligned rows.
 extern "C" __global__ __launch_bounds__(kThreads) void c3_dz_colsum_bf16(
     const unsigned short* __restrict__ Y, const unsigned short* __restrict__ dY, unsigned short* __restrict__ dZ,
-    float* __restrict__ part, int64_t M, int64_t N, int64_t rows_per_chunk, int relu) {
+    float* __restrict__ part, int64_t M, int64_t N, int64_t rows_per_chunk, int act) {
     const int64_t v = (int64_t)blockIdx.x * kThreads + threadIdx.x;  // vector index within a row
     if (8 * v >= N) return;
     const int64_t chunk = blockIdx.y;
@@ -93,7 +132,19 @@ extern "C" __global__ __launch_bounds__(kThreads) void c3_dz_colsum_bf16(
     for (int64_t i = r0; i < r1; ++i) {
         const int64_t off = i * N + 8 * v;
         u32x4 d = *(const u32x4*)(dY + off);
-        if (relu) d = mask_mul8(*(const u32x4*)(Y + off), d);
+        if (act == 1) {
+            d = mask_mul8(*(const u32x4*)(Y + off), d);
+        } else if (act == 2 || act == 3) {
+            const u32x4 y = *(const u32x4*)(Y + off);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float lo = act_grad(bf16_to_f32((unsigned short)(y[e] & 0xffff)),
+                                          bf16_to_f32((unsigned short)(d[e] & 0xffff)), act);
+                const float hi = act_grad(bf16_to_f32((unsigned short)(y[e] >> 16)),
+                                          bf16_to_f32((unsigned short)(d[e] >> 16)), act);
+                d[e] = (uint32_t)f32_to_bf16_rne(lo) | ((uint32_t)f32_to_bf16_rne(hi) << 16);
+            }
+        }
         if (dZ) *(u32x4*)(dZ + off) = d;
         if (part) {
 #pragma unroll

@@ -25,13 +25,21 @@ const char* ew_name(int op) {
         case C3HIP_EW_RELU_BWD: return "relu_bwd";
         case C3HIP_EW_NEG: return "neg";
         case C3HIP_EW_SCALE: return "scale";
+        case C3HIP_EW_SIGMOID: return "sigmoid";
+        case C3HIP_EW_TANH: return "tanh";
+        case C3HIP_EW_EXP: return "exp";
+        case C3HIP_EW_LOG: return "log";
+        case C3HIP_EW_SIGMOID_BWD: return "sigmoid_bwd";
+        case C3HIP_EW_TANH_BWD: return "tanh_bwd";
+        case C3HIP_EW_EXP_BWD: return "exp_bwd";
         default: return nullptr;
     }
 }
 
 bool ew_is_binary(int op) {
     return op == C3HIP_EW_ADD || op == C3HIP_EW_SUB || op == C3HIP_EW_MUL || op == C3HIP_EW_DIV ||
-           op == C3HIP_EW_RELU_BWD;
+           op == C3HIP_EW_RELU_BWD || op == C3HIP_EW_SIGMOID_BWD || op == C3HIP_EW_TANH_BWD ||
+           op == C3HIP_EW_EXP_BWD;
 }
 
 // ---- GEMM planning -------------------------------------------------------
@@ -208,12 +216,15 @@ int colsum(const float* in, const float* mask, float* out, int64_t M, int64_t N,
     return rc;
 }
 
-// bf16 backward: one pass forms dZ = mask(Y) * dY in bf16 (stream-ordered
-// workspace) together with the per-chunk column sums for db, then dX and dW
-// run as plain bf16 GEMMs on dZ (the direct-to-LDS kernels cannot apply the
-// mask while loading).  Without ReLU, dZ is dY itself.
-int linear_bwd_bf16(const void* X, const void* W, const void* Y, const void* dY, void* dX, float* dW, float* db,
-                    int64_t M, int64_t K, int64_t N, bool relu, hipStream_t stream) {
+// Backward through a pre-pass: one pass forms dZ = act'(Y) * dY (in the
+// layer's dtype, stream-ordered workspace) together with the per-chunk column
+// sums for db, then dX and dW run as plain GEMMs on dZ.  Used for every bf16
+// backward (the direct-to-LDS kernels cannot apply a mask while loading) and
+// for the fp32 sigmoid/tanh backward (the fp32 GEMMs fuse only the ReLU
+// mask).  Without an activation, dZ is dY itself.
+int linear_bwd_prepass(int dtype, const void* X, const void* W, const void* Y, const void* dY, void* dX, float* dW,
+                       float* db, int64_t M, int64_t K, int64_t N, int act, hipStream_t stream) {
+    const size_t esz = dtype == C3HIP_BF16 ? 2 : 4;
     if (M == 0 || N == 0) {
         if (db && N > 0) {
             hipError_t e = hipMemsetAsync(db, 0, (size_t)N * sizeof(float), stream);
@@ -224,14 +235,14 @@ int linear_bwd_bf16(const void* X, const void* W, const void* Y, const void* dY,
             if (e != hipSuccess) return set_error(C3HIP_ERR_HIP, std::string("hipMemsetAsync: ") + hipGetErrorString(e));
         }
         if (dX && M > 0 && K > 0) {
-            hipError_t e = hipMemsetAsync(dX, 0, (size_t)(M * K) * 2, stream);
+            hipError_t e = hipMemsetAsync(dX, 0, (size_t)(M * K) * esz, stream);
             if (e != hipSuccess) return set_error(C3HIP_ERR_HIP, std::string("hipMemsetAsync: ") + hipGetErrorString(e));
         }
         return C3HIP_OK;
     }
-    if (N % 8 != 0 || !aligned16(Y) || !aligned16(dY))
+    if (dtype == C3HIP_BF16 && (N % 8 != 0 || !aligned16(Y) || !aligned16(dY)))
         return set_error(C3HIP_ERR_UNSUPPORTED, "bf16 backward needs N % 8 == 0 and 16-byte aligned Y, dY");
-    const bool need_dz = relu && (dX || dW);
+    const bool need_dz = act != C3HIP_ACT_NONE && (dX || dW);
     int64_t nchunks = std::min<int64_t>(256, std::max<int64_t>(1, (M + 31) / 32));
     int64_t rows_per_chunk = (M + nchunks - 1) / nchunks;
     nchunks = (M + rows_per_chunk - 1) / rows_per_chunk;
@@ -239,7 +250,7 @@ int linear_bwd_bf16(const void* X, const void* W, const void* Y, const void* dY,
     float* part = nullptr;
     int rc = C3HIP_OK;
     hipError_t e;
-    if (need_dz && (e = hipMallocAsync(&dz, (size_t)(M * N) * 2, stream)) != hipSuccess)
+    if (need_dz && (e = hipMallocAsync(&dz, (size_t)(M * N) * esz, stream)) != hipSuccess)
         return set_error(C3HIP_ERR_HIP, std::string("hipMallocAsync(dZ): ") + hipGetErrorString(e));
     if (db && nchunks > 1 && (e = hipMallocAsync((void**)&part, (size_t)(nchunks * N) * sizeof(float), stream)) != hipSuccess) {
         if (dz) (void)hipFreeAsync(dz, stream);
@@ -247,10 +258,15 @@ int linear_bwd_bf16(const void* X, const void* W, const void* Y, const void* dY,
     }
     if (need_dz || db) {
         float* part_out = db ? (nchunks > 1 ? part : db) : nullptr;
-        int relu_i = relu ? 1 : 0;
-        const unsigned gx = (unsigned)((N / 8 + 255) / 256);
-        void* args[] = {(void*)&Y, (void*)&dY, &dz, &part_out, &M, &N, &rows_per_chunk, &relu_i};
-        rc = launch("c3_dz_colsum_bf16", dim3(gx, (unsigned)nchunks), dim3(256), args, stream);
+        int act_i = act;
+        void* args[] = {(void*)&Y, (void*)&dY, &dz, &part_out, &M, &N, &rows_per_chunk, &act_i};
+        if (dtype == C3HIP_BF16) {
+            const unsigned gx = (unsigned)((N / 8 + 255) / 256);
+            rc = launch("c3_dz_colsum_bf16", dim3(gx, (unsigned)nchunks), dim3(256), args, stream);
+        } else {
+            const unsigned gx = (unsigned)((N + 255) / 256);
+            rc = launch("c3_dz_colsum_f32", dim3(gx, (unsigned)nchunks), dim3(256), args, stream);
+        }
         if (rc == C3HIP_OK && db && nchunks > 1) {
             void* args2[] = {(void*)&part, (void*)&db, &nchunks, &N};
             rc = launch("c3_colsum_final_f32", dim3((unsigned)((N + 255) / 256)), dim3(256), args2, stream);
@@ -262,14 +278,14 @@ int linear_bwd_bf16(const void* X, const void* W, const void* Y, const void* dY,
         a.A = dzp; a.B = W; a.C = dX;
         a.M = M; a.N = K; a.K = N;
         a.lda = N; a.ldb = N; a.ldc = K;
-        rc = run_gemm(C3HIP_BF16, Kind::Dx, a, true, true, stream);
+        rc = run_gemm(dtype, Kind::Dx, a, true, true, stream);
     }
     if (rc == C3HIP_OK && dW) {
         GemmArgs a{};
         a.A = X; a.B = dzp; a.C = dW;
         a.M = K; a.N = N; a.K = M;
         a.lda = K; a.ldb = N; a.ldc = N;
-        rc = run_gemm(C3HIP_BF16, Kind::Dw, a, false, false, stream);
+        rc = run_gemm(dtype, Kind::Dw, a, false, false, stream);
     }
     if (dz) (void)hipFreeAsync(dz, stream);
     if (part) (void)hipFreeAsync(part, stream);
@@ -316,6 +332,21 @@ int c3hip_elementwise(int op, int dtype, const void* a, const void* b, float alp
     return launch(name, dim3((unsigned)blocks), dim3(256), args, stream);
 }
 
+int c3hip_elementwise3(int op, int dtype, const void* a, const void* b, const void* c, void* out, int64_t n,
+                       void* stream) {
+    clear_error();
+    if (op != C3HIP_EW3_DIV_BWD_B) return set_error(C3HIP_ERR_INVALID, "unknown three-input op " + std::to_string(op));
+    int rc = check_dtype(dtype);
+    if (rc) return rc;
+    if (dtype != C3HIP_F32) return set_error(C3HIP_ERR_UNSUPPORTED, "elementwise ops take fp32 only");
+    if (n < 0) return set_error(C3HIP_ERR_INVALID, "n < 0");
+    if (n == 0) return C3HIP_OK;
+    if (!a || !b || !c || !out) return set_error(C3HIP_ERR_INVALID, "null pointer");
+    const int64_t blocks = std::min<int64_t>((n + 255) / 256, 1 << 16);
+    void* args[] = {(void*)&a, (void*)&b, (void*)&c, &out, &n};
+    return launch("c3_ew3_div_bwd_b_f32", dim3((unsigned)blocks), dim3(256), args, (hipStream_t)stream);
+}
+
 int c3hip_matmul(int dtype, const void* A, const void* B, void* C, int64_t M, int64_t K, int64_t N, int transA,
                  int transB, void* stream) {
     clear_error();
@@ -343,7 +374,7 @@ int c3hip_linear_fwd(int dtype, const void* X, const void* W, const float* b, vo
     clear_error();
     int rc = check_dtype(dtype);
     if (rc) return rc;
-    if (act != C3HIP_ACT_NONE && act != C3HIP_ACT_RELU) return set_error(C3HIP_ERR_INVALID, "unknown act");
+    if (act < C3HIP_ACT_NONE || act > C3HIP_ACT_TANH) return set_error(C3HIP_ERR_INVALID, "unknown act");
     if ((rc = check_elems("X", M, K)) || (rc = check_elems("W", K, N)) || (rc = check_elems("Y", M, N))) return rc;
     if (M > 0 && N > 0 && (!Y || (K > 0 && (!X || !W)))) return set_error(C3HIP_ERR_INVALID, "null pointer");
     GemmArgs a{};
@@ -360,13 +391,14 @@ int c3hip_linear_bwd(int dtype, const void* X, const void* W, const void* Y, con
     hipStream_t stream = (hipStream_t)stream_;
     int rc = check_dtype(dtype);
     if (rc) return rc;
-    if (act != C3HIP_ACT_NONE && act != C3HIP_ACT_RELU) return set_error(C3HIP_ERR_INVALID, "unknown act");
+    if (act < C3HIP_ACT_NONE || act > C3HIP_ACT_TANH) return set_error(C3HIP_ERR_INVALID, "unknown act");
     if ((rc = check_elems("X", M, K)) || (rc = check_elems("W", K, N)) || (rc = check_elems("dY", M, N))) return rc;
     const bool relu = act == C3HIP_ACT_RELU;
-    if (M > 0 && N > 0 && (!dY || (relu && !Y))) return set_error(C3HIP_ERR_INVALID, "null dY / Y");
+    if (M > 0 && N > 0 && (!dY || (act != C3HIP_ACT_NONE && !Y))) return set_error(C3HIP_ERR_INVALID, "null dY / Y");
     if (dX && K > 0 && M > 0 && N > 0 && !W) return set_error(C3HIP_ERR_INVALID, "dX needs W");
     if (dW && K > 0 && N > 0 && M > 0 && !X) return set_error(C3HIP_ERR_INVALID, "dW needs X");
-    if (dtype == C3HIP_BF16) return linear_bwd_bf16(X, W, Y, dY, dX, dW, db, M, K, N, relu, stream);
+    if (dtype == C3HIP_BF16 || act == C3HIP_ACT_SIGMOID || act == C3HIP_ACT_TANH)
+        return linear_bwd_prepass(dtype, X, W, Y, dY, dX, dW, db, M, K, N, act, stream);
     const void* mask = relu ? Y : nullptr;
     if (dX) {
         // dX[M,K] = dZ[M,N] . W^T : logical (M, N=K, K=N), A = dY (k-contig), B(k=n, j) = W[j*N + n].

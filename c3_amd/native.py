@@ -19,10 +19,16 @@ LIB_PATH = LIB_DIR / "libc3hip.so"
 # Status codes, element types, activations and elementwise ops (include/c3hip.h).
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP, ERR_NOT_FOUND, ERR_TOO_LARGE = 0, 1, 2, 3, 4, 5
 F32, BF16 = 0, 1
-ACT_NONE, ACT_RELU = 0, 1
+ACT_NONE, ACT_RELU, ACT_SIGMOID, ACT_TANH = 0, 1, 2, 3
 EW_ADD, EW_SUB, EW_MUL, EW_DIV, EW_RELU, EW_RELU_BWD, EW_NEG, EW_SCALE = range(8)
+EW_SIGMOID, EW_TANH, EW_EXP, EW_LOG, EW_SIGMOID_BWD, EW_TANH_BWD, EW_EXP_BWD = range(8, 15)
+EW3_DIV_BWD_B = 0
+# The eight single-node ops of the fused path's elementwise set.
 EW_OPS = {"add": EW_ADD, "sub": EW_SUB, "mul": EW_MUL, "div": EW_DIV, "relu": EW_RELU,
           "relu_bwd": EW_RELU_BWD, "neg": EW_NEG, "scale": EW_SCALE}
+# Transcendental forward ops and the single-input backward ops.
+EW_MATH_OPS = {"sigmoid": EW_SIGMOID, "tanh": EW_TANH, "exp": EW_EXP, "log": EW_LOG,
+               "sigmoid_bwd": EW_SIGMOID_BWD, "tanh_bwd": EW_TANH_BWD, "exp_bwd": EW_EXP_BWD}
 
 # Every symbol include/c3hip.h declares, with its ctypes signature.
 _vp, _i64, _int, _f = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
@@ -34,6 +40,7 @@ SIGNATURES = {
     "c3hip_load_code_object": (_int, [ctypes.c_char_p, _vp, ctypes.c_size_t]),
     "c3hip_code_object_path": (_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_size_t]),
     "c3hip_elementwise": (_int, [_int, _int, _vp, _vp, _f, _vp, _i64, _i64, _vp]),
+    "c3hip_elementwise3": (_int, [_int, _int, _vp, _vp, _vp, _vp, _i64, _vp]),
     "c3hip_matmul": (_int, [_int, _vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _vp]),
     "c3hip_linear_fwd": (_int, [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _vp]),
     "c3hip_linear_bwd": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _vp]),
@@ -98,6 +105,10 @@ def shutdown() -> None:
 def elementwise(op: int, dtype: int, a: int, b: int | None, alpha: float, out: int, n: int, bmod: int = 0,
                 stream: int = 0) -> None:
     _check("c3hip_elementwise", load().c3hip_elementwise(op, dtype, a, b, alpha, out, n, bmod, stream))
+
+
+def elementwise3(op: int, dtype: int, a: int, b: int, c: int, out: int, n: int, stream: int = 0) -> None:
+    _check("c3hip_elementwise3", load().c3hip_elementwise3(op, dtype, a, b, c, out, n, stream))
 
 
 def matmul(dtype: int, A: int, B: int, C: int, M: int, K: int, N: int, transA: bool = False,

@@ -40,9 +40,12 @@ extern "C" {
 #define C3HIP_F32 0
 #define C3HIP_BF16 1  /* storage bf16 (uint16 bit patterns), fp32 accumulation */
 
-/* Activations (the reference's c3.matmul `act` attribute, include/C3/C3Ops.td:43-87). */
+/* Activations (the reference's c3.matmul `act` attribute, include/C3/C3Ops.td:43-87;
+ * src/C3/C3DialectLowering.cpp:577-589). */
 #define C3HIP_ACT_NONE 0
 #define C3HIP_ACT_RELU 1
+#define C3HIP_ACT_SIGMOID 2 /* 1 / (1 + expf(-z)) */
+#define C3HIP_ACT_TANH 3    /* tanhf(z) */
 
 /* Elementwise ops. */
 #define C3HIP_EW_ADD 0
@@ -53,6 +56,18 @@ extern "C" {
 #define C3HIP_EW_RELU_BWD 5 /* out = (a > 0 ? 1 : 0) * b  (a = forward input, b = grad) */
 #define C3HIP_EW_NEG 6
 #define C3HIP_EW_SCALE 7    /* out = a * alpha */
+#define C3HIP_EW_SIGMOID 8  /* 1 / (1 + expf(-a))      (SigmoidOpLowering, src/C3/C3DialectLowering.cpp:352-380) */
+#define C3HIP_EW_TANH 9     /* tanhf(a)                (UnaryOpLowering<TanhOp>, :321) */
+#define C3HIP_EW_EXP 10     /* expf(a)                 (:322) */
+#define C3HIP_EW_LOG 11     /* logf(a)                 (:323) */
+/* Backward of a single-input node from its forward input a = x and b = grad: */
+#define C3HIP_EW_SIGMOID_BWD 12 /* s = 1/(1+expf(-x)); grad * (s * (1 - s))   (src/C3/C3BackwardCapture.cpp:530-567) */
+#define C3HIP_EW_TANH_BWD 13    /* t = (e^x - e^-x)/(e^x + e^-x); grad * (1 - t*t)   (:569-616) */
+#define C3HIP_EW_EXP_BWD 14     /* expf(x) * grad                            (:823-849) */
+
+/* Three-input elementwise ops (c3hip_elementwise3). */
+#define C3HIP_EW3_DIV_BWD_B 0   /* -((a / (b * b)) * c): Div's gradient for its divisor,
+                                   a = dividend, b = divisor, c = grad (buildDivBackwardGraph) */
 
 /* ABI version of the loaded library (C3HIP_ABI_VERSION). */
 int c3hip_abi_version(void);
@@ -95,7 +110,10 @@ int c3hip_code_object_path(const char* module_name, char* buf, size_t buflen);
  * Elementwise op over n contiguous elements: out[i] = op(a[li], b[ri]).
  * bmod > 0: ri = i mod bmod (rhs broadcast, e.g. a bias row); bmod < 0:
  * li = i mod -bmod (lhs broadcast); 0: no broadcast.  b is ignored (may be
- * NULL) for relu/neg/scale; alpha is used by scale only.  dtype: C3HIP_F32.
+ * NULL) for the unary ops (relu, neg, scale, sigmoid, tanh, exp, log);
+ * alpha is used by scale only.  dtype: C3HIP_F32.  exp/log/tanh are the
+ * device library's expf/logf/tanhf (not bit-identical to a host libm; within
+ * a few ulp of it).
  * Replaces the single-node C3KernelFunc kernels: BinaryOpLowering /
  * UnaryOpLowering / ReLUOpLowering (src/C3/C3DialectLowering.cpp:246-350)
  * dispatched by ConcreteCompiledKernel::execute (src/C3/C3Engine.cpp:457-522),
@@ -104,6 +122,15 @@ int c3hip_code_object_path(const char* module_name, char* buf, size_t buflen);
  */
 int c3hip_elementwise(int op, int dtype, const void* a, const void* b, float alpha, void* out,
                       int64_t n, int64_t bmod, void* stream);
+
+/*
+ * Three-input elementwise op over n contiguous elements (no broadcast):
+ * out[i] = op(a[i], b[i], c[i]).  dtype: C3HIP_F32.  Replaces the
+ * multi-input backward graphs that need both forward inputs and the grad
+ * (Div in:1, src/C3/C3BackwardCapture.cpp buildDivBackwardGraph).
+ */
+int c3hip_elementwise3(int op, int dtype, const void* a, const void* b, const void* c, void* out, int64_t n,
+                       void* stream);
 
 /*
  * C[M,N] = op(A) . op(B), fp32 accumulation.  transA != 0: A is stored
@@ -122,17 +149,22 @@ int c3hip_matmul(int dtype, const void* A, const void* B, void* C, int64_t M, in
  * b is fp32 (may be NULL: no bias).  C3HIP_F32: X, W, Y fp32.  C3HIP_BF16:
  * X, W, Y bf16, fp32 accumulation, bias and activation applied in fp32, Y
  * rounded to nearest-even once.
- * Replaces the MultiNodeKernelFunc of the MatMul+Add+ReLU region
- * (inputs [X, W, b], buildMultiNodeMLIR + buildFusedMultiNode,
- * src/C3/MLIRKernelGen.cpp:610-768, :783-1253; executed by
- * MultiNodeCompiledKernel::execute, src/C3/C3Engine.cpp:145-235).
+ * act: C3HIP_ACT_NONE, _RELU (maxnum(z, 0)), _SIGMOID (1 / (1 + expf(-z)),
+ * the fused epilogue's formula, src/C3/MLIRKernelGen.cpp:711-718) or _TANH
+ * (tanhf(z), the c3.matmul act = 3 epilogue, src/C3/C3DialectLowering.cpp:588).
+ * Replaces the MultiNodeKernelFunc of the MatMul+Add+ReLU and
+ * MatMul+Add+Sigmoid regions (inputs [X, W, b], buildMultiNodeMLIR +
+ * buildFusedMultiNode, src/C3/MLIRKernelGen.cpp:610-768, :783-1253; executed
+ * by MultiNodeCompiledKernel::execute, src/C3/C3Engine.cpp:145-235).
  */
 int c3hip_linear_fwd(int dtype, const void* X, const void* W, const float* b, void* Y, int64_t M,
                      int64_t K, int64_t N, int act, void* stream);
 
 /*
  * Fused Linear backward.  With dZ = (Y > 0 ? 1 : 0) * dY when act ==
- * C3HIP_ACT_RELU (dZ = dY when act == C3HIP_ACT_NONE):
+ * C3HIP_ACT_RELU, dY * (Y * (1 - Y)) for C3HIP_ACT_SIGMOID, dY * (1 - Y * Y)
+ * for C3HIP_ACT_TANH (the activation's derivative from its output) and
+ * dZ = dY for C3HIP_ACT_NONE:
  *   dX[M,K] = dZ . W^T,  dW[K,N] = X^T . dZ,  db[N] = sum over rows of dZ.
  * dX, dW and db are each optional (NULL skips it).  dZ is formed inside the
  * GEMM operand loads and never written.  C3HIP_F32: all fp32.  C3HIP_BF16:

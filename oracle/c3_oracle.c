@@ -137,11 +137,25 @@ void oracle_matmul(const float* A, const float* B, float* C, int64_t M, int64_t 
  * Add->ReLU into a FusedNode, src/C3/Graph.cpp:587-772, so the c3.matmul
  * epilogue detection at src/C3/MLIRKernelGen.cpp:1124-1198 never fires).
  * act: 0 = bias only, 1 = bias + ReLU.                                     */
+/* act 2: the fused epilogue's sigmoid, 1 / (1 + expf(-z)) (NegF, expf call,
+ * AddF, DivF; src/C3/MLIRKernelGen.cpp:711-718); act 3: tanhf(z) (math.tanh,
+ * the c3.matmul act = 3 epilogue, src/C3/C3DialectLowering.cpp:588). */
+static float act_fwd(float z, int act) {
+    if (act == 1) return oracle_maxnum(z, 0.0f);
+    if (act == 2) {
+        float e = expf(-z);
+        float d = 1.0f + e;
+        return 1.0f / d;
+    }
+    if (act == 3) return tanhf(z);
+    return z;
+}
+
 void oracle_bias_act(const float* t, const float* bias, float* y, int64_t M, int64_t N, int act) {
     for (int64_t i = 0; i < M; ++i) {
         for (int64_t j = 0; j < N; ++j) {
             float z = t[i * N + j] + bias[j];
-            y[i * N + j] = act == 1 ? oracle_maxnum(z, 0.0f) : z;
+            y[i * N + j] = act_fwd(z, act);
         }
     }
 }
@@ -203,6 +217,8 @@ void oracle_linear_bwd(const float* X, const float* W, const float* Y, const flo
     float* dz = (float*)malloc((size_t)(M * N) * sizeof(float));
     if (act == 1)
         oracle_relu_mask_mul(Y, dY, dz, M * N);
+    else if (act == 2 || act == 3)
+        oracle_act_grad(Y, dY, dz, M * N, act);
     else
         memcpy(dz, dY, (size_t)(M * N) * sizeof(float));
     /* dX[M,K] = dZ[M,N] . W[K,N]^T : matmul with M'=M, K'=N, N'=K, transB.  */
@@ -237,7 +253,82 @@ void oracle_elementwise(int op, const float* a, const float* b, float alpha, flo
             case ORACLE_EW_RELU_BWD: r = ((x > 0.0f) ? 1.0f : 0.0f) * b[ri]; break;
             case ORACLE_EW_NEG: r = -x; break;
             case ORACLE_EW_SCALE: r = x * alpha; break;
+            /* SigmoidOpLowering (src/C3/C3DialectLowering.cpp:352-380): NegF, math.exp,
+             * AddF(1, e), DivF(1, d); Tanh/Exp/Log: math.tanh/exp/log (:321-323). */
+            case ORACLE_EW_SIGMOID: {
+                float e = expf(-x);
+                float d = 1.0f + e;
+                r = 1.0f / d;
+                break;
+            }
+            case ORACLE_EW_TANH: r = tanhf(x); break;
+            case ORACLE_EW_EXP: r = expf(x); break;
+            case ORACLE_EW_LOG: r = logf(x); break;
+            /* buildSigmoidBackwardGraph (src/C3/C3BackwardCapture.cpp:530-567):
+             * s = 1/(1+exp(-x)), one_minus = 1 - s, t = s * one_minus, grad * t. */
+            case ORACLE_EW_SIGMOID_BWD: {
+                float e = expf(-x);
+                float d = 1.0f + e;
+                float s = 1.0f / d;
+                float om = 1.0f - s;
+                float t = s * om;
+                r = b[ri] * t;
+                break;
+            }
+            /* buildTanhBackwardGraph (:569-616): tanh through exp,
+             * (e^x - e^-x) / (e^x + e^-x), then grad * (1 - t*t). */
+            case ORACLE_EW_TANH_BWD: {
+                float e = expf(x);
+                float en = expf(-x);
+                float num = e - en;
+                float den = e + en;
+                float t = num / den;
+                float sq = t * t;
+                float om = 1.0f - sq;
+                r = b[ri] * om;
+                break;
+            }
+            /* buildExpBackwardGraph (:823-849): exp(x) * grad. */
+            case ORACLE_EW_EXP_BWD: r = expf(x) * b[ri]; break;
             default: r = NAN; break;
+        }
+        out[i] = r;
+    }
+}
+
+/* buildDivBackwardGraph, input 1: b_sq = B * B, q = A / b_sq, m = q * grad, -m. */
+void oracle_elementwise3(int op, const float* a, const float* b, const float* c, float* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) {
+        float r = NAN;
+        if (op == ORACLE_EW3_DIV_BWD_B) {
+            float bb = b[i] * b[i];
+            float q = a[i] / bb;
+            float m = q * c[i];
+            r = -m;
+        }
+        out[i] = r;
+    }
+}
+
+/* The activation's derivative applied to the incoming gradient, from the
+ * activation's output y: ReLU (y > 0 ? 1 : 0) * g (buildReLUBackwardGraph with
+ * z > 0 <=> y > 0); sigmoid g * (y * (1 - y)) (buildSigmoidBackwardGraph: its
+ * recomputed s from the pre-activation equals y); tanh g * (1 - y * y). */
+void oracle_act_grad(const float* y, const float* g, float* out, int64_t n, int act) {
+    for (int64_t i = 0; i < n; ++i) {
+        float r;
+        if (act == 1) {
+            r = ((y[i] > 0.0f) ? 1.0f : 0.0f) * g[i];
+        } else if (act == 2) {
+            float om = 1.0f - y[i];
+            float t = y[i] * om;
+            r = g[i] * t;
+        } else if (act == 3) {
+            float sq = y[i] * y[i];
+            float om = 1.0f - sq;
+            r = g[i] * om;
+        } else {
+            r = g[i];
         }
         out[i] = r;
     }

@@ -30,8 +30,16 @@ enum {
     ORACLE_EW_RELU = 4,
     ORACLE_EW_RELU_BWD = 5,
     ORACLE_EW_NEG = 6,
-    ORACLE_EW_SCALE = 7
+    ORACLE_EW_SCALE = 7,
+    ORACLE_EW_SIGMOID = 8,
+    ORACLE_EW_TANH = 9,
+    ORACLE_EW_EXP = 10,
+    ORACLE_EW_LOG = 11,
+    ORACLE_EW_SIGMOID_BWD = 12,
+    ORACLE_EW_TANH_BWD = 13,
+    ORACLE_EW_EXP_BWD = 14
 };
+enum { ORACLE_EW3_DIV_BWD_B = 0 };
 
 /* ---- seeded synthetic inputs (SplitMix64) ---- */
 uint64_t oracle_splitmix64_next(uint64_t* state);
@@ -60,6 +68,9 @@ void oracle_linear_bwd(const float* X, const float* W, const float* Y, const flo
                        float* dW, float* db, int64_t M, int64_t K, int64_t N, int act);
 void oracle_elementwise(int op, const float* a, const float* b, float alpha, float* out,
                         int64_t n, int64_t bmod);
+void oracle_elementwise3(int op, const float* a, const float* b, const float* c, float* out, int64_t n);
+/* act'(y) * g from the activation's output y (act 0..3), elementwise. */
+void oracle_act_grad(const float* y, const float* g, float* out, int64_t n, int act);
 
 /* ---- softmax cross-entropy for the MLP train step (host-side step of the caller) ---- */
 float oracle_softmax_ce(const float* logits, const int32_t* labels, float* loss_rows, float* dlogits,

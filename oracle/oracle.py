@@ -18,8 +18,11 @@ _LIB_PATH = _HERE / "liboracle.so"
 _lib = None
 
 EW_ADD, EW_SUB, EW_MUL, EW_DIV, EW_RELU, EW_RELU_BWD, EW_NEG, EW_SCALE = range(8)
-EW_NAMES = ["add", "sub", "mul", "div", "relu", "relu_bwd", "neg", "scale"]
-EW_BINARY = {EW_ADD, EW_SUB, EW_MUL, EW_DIV, EW_RELU_BWD}
+EW_NAMES = ["add", "sub", "mul", "div", "relu", "relu_bwd", "neg", "scale", "sigmoid", "tanh", "exp", "log",
+            "sigmoid_bwd", "tanh_bwd", "exp_bwd"]
+EW_SIGMOID, EW_TANH, EW_EXP, EW_LOG, EW_SIGMOID_BWD, EW_TANH_BWD, EW_EXP_BWD = range(8, 15)
+EW3_DIV_BWD_B = 0
+EW_BINARY = {EW_ADD, EW_SUB, EW_MUL, EW_DIV, EW_RELU_BWD, EW_SIGMOID_BWD, EW_TANH_BWD, EW_EXP_BWD}
 
 _f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
 _i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
@@ -48,6 +51,8 @@ def lib():
         vp = ctypes.c_void_p
         L.oracle_linear_bwd.argtypes = [_f32p, _f32p, _f32p, _f32p, vp, vp, vp, _i64, _i64, _i64, ctypes.c_int]
         L.oracle_elementwise.argtypes = [ctypes.c_int, _f32p, vp, ctypes.c_float, _f32p, _i64, _i64]
+        L.oracle_elementwise3.argtypes = [ctypes.c_int, _f32p, _f32p, _f32p, _f32p, _i64]
+        L.oracle_act_grad.argtypes = [_f32p, _f32p, _f32p, _i64, ctypes.c_int]
         L.oracle_softmax_ce.argtypes = [_f32p, _i32p, vp, vp, _i64, _i64]
         L.oracle_softmax_ce.restype = ctypes.c_float
         L.oracle_sgd_update.argtypes = [_f32p, _f32p, ctypes.c_float, _i64]
@@ -170,6 +175,20 @@ def elementwise(op, a, b=None, alpha=0.0, bmod=0):
     bb = None if b is None else _c(b).reshape(-1)
     out = np.empty(n, dtype=np.float32)
     lib().oracle_elementwise(op, a, _ptr(bb), alpha, out, n, bmod)
+    return out
+
+
+def elementwise3(op, a, b, c):
+    a, b, c = _c(a).reshape(-1), _c(b).reshape(-1), _c(c).reshape(-1)
+    out = np.empty(a.size, dtype=np.float32)
+    lib().oracle_elementwise3(op, a, b, c, out, a.size)
+    return out
+
+
+def act_grad(y, g, act):
+    y, g = _c(y), _c(g)
+    out = np.empty_like(y)
+    lib().oracle_act_grad(y.reshape(-1), g.reshape(-1), out.reshape(-1), y.size, act)
     return out
 
 

@@ -455,6 +455,57 @@ TEST(region_registry_install_and_match) {
     CHECK(!RF.mayMatchAsLastOp(op::ReLU));
 }
 
+// ------------------------------------------------ activation specs ------
+TEST(sigmoid_tanh_exp_log_specs) {
+    KernelSpec s;
+    using R = C3HotPathManager::DispatchRecord;
+    CHECK(C3HotPathManager::buildFusedSpec({R{op::MatMul, {8, 4, 4, 6}, {8, 4}, {4, 6}, DType::kFloat, {}},
+                                            R{op::Add, {8, 6, 6}, {8, 6}, {6}, DType::kFloat, {}},
+                                            R{op::Sigmoid, {8, 6}, {8, 6}, {}, DType::kFloat, {}}},
+                                           "MatMul+Add+Sigmoid", &s));
+    CHECK(s.kind == KernelKind::LinearFwd && s.act == C3HIP_ACT_SIGMOID && s.input_shapes.size() == 3);
+    CHECK(C3HotPathManager::buildFusedSpec({R{op::MatMul, {8, 4, 4, 6}, {8, 4}, {4, 6}, DType::kFloat, {}},
+                                            R{op::Sigmoid, {8, 6}, {8, 6}, {}, DType::kFloat, {}}},
+                                           "MatMul+Sigmoid", &s));
+    CHECK(s.act == C3HIP_ACT_SIGMOID && s.input_shapes.size() == 2);  // no bias
+    const std::pair<op, int> unary[] = {{op::Sigmoid, C3HIP_EW_SIGMOID}, {op::Tanh, C3HIP_EW_TANH},
+                                        {op::Exp, C3HIP_EW_EXP}, {op::Log, C3HIP_EW_LOG}};
+    for (auto [o, code] : unary) {
+        CHECK(C3HotPathManager::isSupportedOp(o));
+        CHECK(C3HotPathManager::buildSingleOpSpec(o, {4, 5}, {}, DType::kFloat, &s));
+        CHECK(s.kind == KernelKind::Elementwise && s.ew_op == code && s.input_shapes.size() == 1);
+    }
+    CHECK(!C3HotPathManager::isSupportedOp(op::Cos));
+}
+
+TEST(backward_rules_of_elementwise_nodes) {
+    KernelSpec s;
+    std::vector<size_t> map;
+    size_t n = 0;
+    const std::vector<size_t> g = {4, 6};
+    auto build = [&](const char* t, std::vector<std::vector<size_t>> in, size_t i) {
+        return C3BackwardCapture::buildBackwardSpecForInput(t, g, in, DType::kFloat, i, &s, &map, &n);
+    };
+    CHECK(build("Sigmoid", {g}, 0) && s.kind == KernelKind::UnaryBackward && s.ew_op == C3HIP_EW_SIGMOID_BWD &&
+          map == std::vector<size_t>{0} && n == 2);
+    CHECK(build("Tanh", {g}, 0) && s.ew_op == C3HIP_EW_TANH_BWD);
+    CHECK(build("Exp", {g}, 0) && s.ew_op == C3HIP_EW_EXP_BWD);
+    CHECK(!build("Exp", {g}, 1));
+    CHECK(build("Log", {g}, 0) && s.kind == KernelKind::Elementwise && s.ew_op == C3HIP_EW_DIV && n == 2);
+    CHECK(build("Neg", {g}, 0) && s.ew_op == C3HIP_EW_NEG && map.empty() && n == 1);
+    CHECK(build("Sub", {g, g}, 0) && s.kind == KernelKind::AddBackwardLhs);
+    CHECK(build("Sub", {g, g}, 1) && s.kind == KernelKind::Elementwise && s.ew_op == C3HIP_EW_NEG);
+    CHECK(build("Mul", {g, g}, 0) && s.ew_op == C3HIP_EW_MUL && map == std::vector<size_t>{1});
+    CHECK(build("Mul", {g, g}, 1) && s.ew_op == C3HIP_EW_MUL && map == std::vector<size_t>{0});
+    CHECK(build("Div", {g, g}, 0) && s.ew_op == C3HIP_EW_DIV && map == std::vector<size_t>{1});
+    CHECK(build("Div", {g, g}, 1) && s.kind == KernelKind::DivBackwardB && map == (std::vector<size_t>{0, 1}) &&
+          n == 3);
+    CHECK(!build("Mul", {g, {6}}, 0));  // broadcast operand: not compiled
+    CHECK(!build("Cos", {g}, 0));
+    for (const char* t : {"Sigmoid", "Tanh", "Exp", "Log", "Neg", "Sub", "Mul", "Div"})
+        CHECK(C3BackwardCapture::supportsNodeType(t));
+}
+
 // ---------------------------------------------------------------- engine ---
 TEST(engine_cache_and_watchdog) {
     HostBackend hb;
@@ -512,7 +563,7 @@ TEST(hotpath_threshold_dual_tier_install) {
     CHECK(H.getStats().cooldown_hits >= 1);
     // MPS calls are ignored; unsupported ops trigger but build nothing.
     H.recordCall(op::Add, DeviceType::kMPS, {9}, {9});
-    for (int i = 0; i < 5; ++i) H.recordCall(op::Tanh, DeviceType::kCPU, {4});
+    for (int i = 0; i < 5; ++i) H.recordCall(op::Cos, DeviceType::kCPU, {4});
     H.waitForPendingCompiles();
     CHECK_EQ(g_built.load(), 2);
 }
@@ -554,13 +605,19 @@ TEST(hotpath_fused_pattern_installs_region) {
     }
     H.waitForPendingCompiles();
     CHECK_EQ(g_built.load(), built);
-    // Sigmoid epilogue: detected, no kernel.
+    // Sigmoid epilogue: a region kernel too.
     H.recordCall(op::MatMul, DeviceType::kCPU, {5, 4}, {4, 2}, true);
     H.recordCall(op::Add, DeviceType::kCPU, {5, 2}, {2}, true);
     H.recordCall(op::Sigmoid, DeviceType::kCPU, {5, 2}, {}, true);
     H.waitForPendingCompiles();
+    CHECK_EQ(g_built.load(), built + 1);
+    // A full-tensor Add (not a bias row) is detected but has no fused kernel.
+    H.recordCall(op::MatMul, DeviceType::kCPU, {6, 4}, {4, 2}, true);
+    H.recordCall(op::Add, DeviceType::kCPU, {6, 2}, {6, 2}, true);
+    H.recordCall(op::Sigmoid, DeviceType::kCPU, {6, 2}, {}, true);
+    H.waitForPendingCompiles();
     CHECK(H.getStats().patterns_unsupported >= 1);
-    CHECK_EQ(g_built.load(), built);
+    CHECK_EQ(g_built.load(), built + 1);
 }
 
 TEST(hotpath_spec_builders) {
@@ -570,7 +627,8 @@ TEST(hotpath_spec_builders) {
     CHECK(C3HotPathManager::buildSingleOpSpec(op::MatMul, {8, 4}, {4, 2}, DType::kBFloat16, &s));
     CHECK(s.kind == KernelKind::MatMul && s.out_shape == (std::vector<size_t>{8, 2}) && s.moduleName() == "gemm_bf16");
     CHECK(!C3HotPathManager::buildSingleOpSpec(op::MatMul, {8, 4}, {3, 2}, DType::kFloat, &s));
-    CHECK(!C3HotPathManager::buildSingleOpSpec(op::Sigmoid, {8}, {}, DType::kFloat, &s));
+    CHECK(!C3HotPathManager::buildSingleOpSpec(op::Cos, {8}, {}, DType::kFloat, &s));
+    CHECK(!C3HotPathManager::buildSingleOpSpec(op::Sigmoid, {8}, {}, DType::kBFloat16, &s));
     using R = C3HotPathManager::DispatchRecord;
     std::vector<R> recs = {R{op::MatMul, {8, 4, 4, 2}, {8, 4}, {4, 2}, DType::kFloat, {}},
                            R{op::Add, {8, 2, 2}, {8, 2}, {2}, DType::kFloat, {}},

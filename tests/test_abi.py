@@ -53,8 +53,10 @@ def test_code_objects_hold_every_dispatched_kernel():
             for v in "vs":
                 assert f"c3_gemm_f32_{kind}_{tile}_{v}" in gemm
     ew = _kernel_symbols(LIB / "elementwise.hsaco")
-    for op in native.EW_OPS:
+    for op in list(native.EW_OPS) + list(native.EW_MATH_OPS):
         assert f"c3_ew_{op}_f32_v" in ew and f"c3_ew_{op}_f32_s" in ew
+    assert "c3_ew3_div_bwd_b_f32" in ew
+    assert {"c3_dz_colsum_f32", "c3_dz_colsum_bf16"} <= _kernel_symbols(LIB / "reduce.hsaco")
     red = _kernel_symbols(LIB / "reduce.hsaco")
     assert {"c3_colsum_partial_f32", "c3_colsum_final_f32", "c3_rowsum_f32"} <= red
     loss = _kernel_symbols(LIB / "loss.hsaco")
@@ -93,6 +95,16 @@ def test_gemm_validation():
     assert _rc("c3hip_linear_bwd", 0, None, None, None, 16, 16, None, None, 4, 4, 4, 0, None) == native.ERR_INVALID
     assert _rc("c3hip_sum_reduce", 16, 16, 4, 4, 2, None) == native.ERR_INVALID
     assert _rc("c3hip_sum_reduce", None, 16, 4, 0, 0, None) == native.OK
+
+
+def test_elementwise3_and_act_validation():
+    assert _rc("c3hip_elementwise3", 5, 0, 16, 16, 16, 16, 4, None) == native.ERR_INVALID
+    assert _rc("c3hip_elementwise3", 0, native.BF16, 16, 16, 16, 16, 4, None) == native.ERR_UNSUPPORTED
+    assert _rc("c3hip_elementwise3", 0, 0, 16, None, 16, 16, 4, None) == native.ERR_INVALID
+    assert _rc("c3hip_elementwise3", 0, 0, None, None, None, None, 0, None) == native.OK
+    assert _rc("c3hip_elementwise", 15, 0, 16, 16, 0.0, 16, 4, 0, None) == native.ERR_INVALID
+    assert _rc("c3hip_linear_fwd", 0, 16, 16, None, 16, 4, 4, 4, 4, None) == native.ERR_INVALID  # act 4
+    assert _rc("c3hip_linear_bwd", 0, 16, 16, None, 16, 16, None, None, 4, 4, 4, 2, None) == native.ERR_INVALID
 
 
 def test_train_step_helper_validation():

@@ -351,3 +351,97 @@ def test_sgd_update_rounds_the_product_first():
     wb = O.pack_bf16(np.array([1.0, 1.5], np.float32))
     ob = O.sgd_update(wb, np.array([2.0 ** -8, 0.25], np.float32), 0.5)
     assert np.array_equal(O.bf16_bits_to_f32(ob), np.array([1.0, 1.375], np.float32))
+
+
+
+# ------------------------------------------------- transcendental ops ----
+def _ulp(x):
+    x = np.abs(np.asarray(x, np.float64))
+    return np.maximum(np.spacing(x.astype(np.float32)).astype(np.float64), np.finfo(np.float32).tiny)
+
+
+def test_transcendental_ops_against_float64():
+    # libm's expf/logf/tanhf are within an ulp or two of the exact value; the
+    # sigmoid chain adds an add and a division.
+    x = np.concatenate([np.linspace(-20, 20, 4001), O.normal(91, 4000, 0.0, 3.0)]).astype(np.float32)
+    xd = x.astype(np.float64)
+    checks = {
+        O.EW_EXP: (np.exp(xd), 1.0),
+        O.EW_TANH: (np.tanh(xd), 2.0),
+        O.EW_SIGMOID: (1.0 / (1.0 + np.exp(-xd)), 3.0),
+    }
+    for op, (exact, k) in checks.items():
+        got = O.elementwise(op, x).astype(np.float64)
+        assert np.all(np.abs(got - exact) <= k * _ulp(exact)), O.EW_NAMES[op]
+    pos = np.abs(x) + np.float32(1e-3)
+    got = O.elementwise(O.EW_LOG, pos).astype(np.float64)
+    exact = np.log(pos.astype(np.float64))
+    assert np.all(np.abs(got - exact) <= 1.0 * _ulp(exact))
+
+
+def test_transcendental_closed_forms_and_specials():
+    z = np.zeros(1, np.float32)
+    assert O.elementwise(O.EW_SIGMOID, z)[0] == 0.5
+    assert O.elementwise(O.EW_EXP, z)[0] == 1.0 and O.elementwise(O.EW_TANH, z)[0] == 0.0
+    assert O.elementwise(O.EW_LOG, np.ones(1, np.float32))[0] == 0.0
+    g = np.array([3.0], np.float32)
+    assert O.elementwise(O.EW_SIGMOID_BWD, z, g)[0] == np.float32(0.75)   # 3 * 0.25
+    assert O.elementwise(O.EW_TANH_BWD, z, g)[0] == 3.0                  # t = 0
+    assert O.elementwise(O.EW_EXP_BWD, z, g)[0] == 3.0
+    big = np.array([-200.0, 200.0], np.float32)
+    with np.errstate(all="ignore"):
+        assert np.array_equal(O.elementwise(O.EW_SIGMOID, big), np.array([0.0, 1.0], np.float32))
+        assert np.isinf(O.elementwise(O.EW_EXP, big)[1]) and O.elementwise(O.EW_EXP, big)[0] == 0.0
+        assert O.elementwise(O.EW_LOG, np.zeros(1, np.float32))[0] == -np.inf
+        assert np.isnan(O.elementwise(O.EW_LOG, -np.ones(1, np.float32))[0])
+        # Tanh backward goes through exp like the reference: inf / inf for |x| > ~88.7.
+        assert np.all(np.isnan(O.elementwise(O.EW_TANH_BWD, big, np.ones(2, np.float32))))
+    # Div's divisor gradient: -((a / (b * b)) * g), exact on powers of two.
+    a, b, c = (np.array(v, np.float32) for v in ([1.0, -6.0], [2.0, 0.5], [8.0, 1.0]))
+    assert np.array_equal(O.elementwise3(O.EW3_DIV_BWD_B, a, b, c), np.array([-2.0, 24.0], np.float32))
+
+
+def test_backward_ops_follow_the_reference_graph_order():
+    # Sigmoid backward is grad * (s * (1 - s)) and tanh backward recomputes
+    # tanh through exp; on random inputs some results differ in the last bit
+    # from (grad * s) * (1 - s) and from 1 - tanhf(x)^2, so these pin the order.
+    x = O.normal(92, 20000, 0.0, 2.0)
+    g = O.normal(93, 20000, 0.0, 3.0)
+    f = np.float32
+    with np.errstate(all="ignore"):
+        e = np.exp(-x.astype(np.float64)).astype(f)
+    s = (f(1.0) / (f(1.0) + e)).astype(f)
+    want = (g * (s * (f(1.0) - s))).astype(f)
+    other = ((g * s) * (f(1.0) - s)).astype(f)
+    got = O.elementwise(O.EW_SIGMOID_BWD, x, g)
+    exp_ok = O.elementwise(O.EW_EXP, -x)
+    same_e = exp_ok == e   # where libm's expf agrees with numpy's rounding of exp
+    assert np.array_equal(got[same_e], want[same_e])
+    assert np.any(got[same_e] != other[same_e])
+    t_tanhf = O.elementwise(O.EW_TANH, x)
+    gt = O.elementwise(O.EW_TANH_BWD, x, g)
+    via_tanhf = (g * (f(1.0) - t_tanhf * t_tanhf)).astype(f)
+    assert np.any(gt != via_tanhf)
+    bound = np.abs(g).astype(np.float64) * 16 * 2.0 ** -23 + 4 * _ulp(via_tanhf)
+    assert np.all(np.abs(gt.astype(np.float64) - via_tanhf) <= bound)
+
+
+def test_act_grad_and_epilogue_activations():
+    y = np.array([0.0, 0.5, 0.25, -0.5, 2.0], np.float32)
+    g = np.array([1.0, 1.0, 2.0, 4.0, -1.0], np.float32)
+    assert np.array_equal(O.act_grad(y, g, 1), O.relu_mask_mul(y, g))
+    assert np.array_equal(O.act_grad(y, g, 2), g * (y * (np.float32(1) - y)))
+    assert np.array_equal(O.act_grad(y, g, 3), g * (np.float32(1) - y * y))
+    assert np.array_equal(O.act_grad(y, g, 0), g)
+    assert O.act_grad(np.float32([0.5]), np.float32([1.0]), 2)[0] == 0.25
+    # Sigmoid/tanh epilogues equal the elementwise ops applied to t + b.
+    t = O.normal(94, (16, 24), 0.0, 2.0)
+    b = O.normal(95, 24)
+    z = O.bias_act(t, b, act=0)
+    assert np.array_equal(O.bias_act(t, b, act=2), O.elementwise(O.EW_SIGMOID, z).reshape(z.shape))
+    assert np.array_equal(O.bias_act(t, b, act=3), O.elementwise(O.EW_TANH, z).reshape(z.shape))
+    # The fused sigmoid backward from Y equals the per-node backward from Z
+    # (the per-node graph recomputes the same s = 1/(1+exp(-z))).
+    gz = O.normal(96, z.shape)
+    y2 = O.bias_act(t, b, act=2)
+    assert np.array_equal(O.act_grad(y2, gz, 2), O.elementwise(O.EW_SIGMOID_BWD, z, gz).reshape(z.shape))
