@@ -166,7 +166,7 @@ def main():
         out["elementwise"] = {"2^28": bench_elementwise(torch, C, dev, s, 1 << 28, sets=1),
                               "2^24": bench_elementwise(torch, C, dev, s, 1 << 24, sets=8)}
         out["mlp_784_256_128_10_fp32"] = bench_mlp(torch, C, dev, s, [784, 256, 128, 10], 128, C.F32,
-                                                   steps=200, uniform_x=True)
+                                                   steps=200, uniform_x=True, graph=True)
         out["mlp_deep_bf16"] = bench_mlp(torch, C, dev, s, [4096, 8192, 8192, 8192, 4096, 1000], 16384, C.BF16,
                                          steps=10, uniform_x=False)
     if not args.no_cpu_baseline:
@@ -296,7 +296,7 @@ def bench_bf16_sweep(torch, C, dev, s, reps=5):
             "median_tflops": vals[len(vals) // 2], "min_tflops": vals[0], "max_tflops": vals[-1]}
 
 
-def bench_mlp(torch, C, dev, s, dims, batch, dtype, steps, uniform_x):
+def bench_mlp(torch, C, dev, s, dims, batch, dtype, steps, uniform_x, graph=False):
     """Train step of an MLP (ReLU between layers, softmax-CE, SGD) through the
     dispatch flow (c3_amd/trainer.py: region kernels from RegionFusionRegistry,
     fused backwards from C3BackwardCapture, JIT cache warm), after warm-up
@@ -335,6 +335,23 @@ def bench_mlp(torch, C, dev, s, dims, batch, dtype, steps, uniform_x):
     ms = e0.elapsed_time(e1) / steps
     loss1 = tr.step(xd.data_ptr(), lbl.data_ptr(), lr, True, s)
     st1 = tr.stats()
+    graph_ms = None
+    if graph:
+        # The same step captured as one HIP graph (on a side stream: the
+        # default stream cannot be captured) and replayed.
+        side = torch.cuda.Stream()
+        with torch.cuda.stream(side):
+            tr.capture(xd.data_ptr(), lbl.data_ptr(), lr, side.cuda_stream)
+            for _ in range(3):
+                tr.replay(side.cuda_stream)
+            g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            side.synchronize()
+            g0.record(side)
+            for _ in range(steps):
+                tr.replay(side.cuda_stream)
+            g1.record(side)
+            side.synchronize()
+        graph_ms = g0.elapsed_time(g1) / steps
     tr.close()
     del keep, x, xd, lbl
     torch.cuda.empty_cache()
@@ -348,7 +365,9 @@ def bench_mlp(torch, C, dev, s, dims, batch, dtype, steps, uniform_x):
             "backward_hits_timed": st1["backward_hits"] - st0["backward_hits"],
             "eager_ops_timed": st1["eager_ops"] - st0["eager_ops"],
             "fully_dispatched": bool(st1["fully_dispatched"]),
-            "loss_before": round(loss0, 5), "loss_after": round(loss1, 5)}
+            "loss_before": round(loss0, 5), "loss_after": round(loss1, 5),
+            **({"graph_replay_us_per_step": round(graph_ms * 1e3, 2),
+                "graph_replay_tflops": round(flop / (graph_ms * 1e-3) / 1e12, 3)} if graph_ms else {})}
 
 
 def cpu_baseline():

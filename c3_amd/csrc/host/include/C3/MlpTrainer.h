@@ -39,6 +39,7 @@ struct MlpStepStats {
     size_t eager_ops = 0;         // forward ops (or bf16 layers) run eagerly
     size_t backward_hits = 0;     // layer backwards run by an installed fused kernel
     size_t backward_misses = 0;   // layer backwards run eagerly
+    size_t graph_replays = 0;     // steps run by replaying the captured graph
 };
 
 class MlpTrainer {
@@ -47,6 +48,9 @@ public:
     // allocated on the current HIP device; W[l] is [dims[l], dims[l+1]]
     // (row-major, [in, out]) in dt, b[l] is fp32 [dims[l+1]].
     MlpTrainer(std::vector<size_t> dims, size_t batch, DType dt);
+    ~MlpTrainer();
+    MlpTrainer(const MlpTrainer&) = delete;
+    MlpTrainer& operator=(const MlpTrainer&) = delete;
 
     size_t numLayers() const { return W_.size(); }
     Tensor& weight(size_t l) { return W_.at(l); }
@@ -68,6 +72,18 @@ public:
     // every layer backward as a fused kernel.
     bool lastStepFullyDispatched() const { return last_fully_dispatched_; }
 
+    // Record one train step (with learning rate lr, inputs X and labels at
+    // their current addresses) as a HIP graph on the current stream, which
+    // must not be the default stream; replay() then runs that step again with
+    // one launch: the same kernels the dispatch flow chose, on the same
+    // buffers (the captured step's intermediates stay allocated).  Call after
+    // warmUp so that every dispatch hits an installed kernel and no compile
+    // or allocation happens during the capture.  The caller refreshes X and
+    // the labels in place between replays.
+    void captureStep(const Tensor& X, const void* labels, float lr);
+    void replay();
+    bool hasGraph() const { return graph_exec_ != nullptr; }
+
     const MlpStepStats& stats() const { return stats_; }
 
     // Keep the last step's gradients for inspection (off by default: holding
@@ -83,6 +99,9 @@ public:
 
 private:
     Tensor layerForwardEager(size_t l, const Tensor& A, bool relu);
+    Tensor make(std::vector<size_t> shape, DType dt);  // device tensor, held while retaining
+    Tensor hold(Tensor t);                              // keep t alive while retaining
+    void releaseGraph();
 
     std::vector<size_t> dims_;
     size_t batch_;
@@ -94,6 +113,11 @@ private:
     MlpStepStats stats_;
     bool last_fully_dispatched_ = false;
     bool keep_grads_ = false;
+    bool retain_ = false;
+    std::vector<Tensor> retained_;
+    void* graph_ = nullptr;       // hipGraph_t
+    void* graph_exec_ = nullptr;  // hipGraphExec_t
+    bool graph_dispatched_ = false;
     std::vector<Tensor> kept_g_, kept_dW_, kept_db_;
     size_t step_region_hits_ = 0, step_bwd_hits_ = 0;
 };
@@ -116,9 +140,12 @@ int c3mlp_forward(c3mlp* m, const void* X, void* logits_out, void* stream);
 int c3mlp_step(c3mlp* m, const void* X, const int32_t* labels, float lr, float* loss_out, void* stream);
 int c3mlp_warm_up(c3mlp* m, const void* X, const int32_t* labels, float lr, int max_steps, int* steps_run,
                   void* stream);
-// out[0..6] = steps, region_hits, single_op_hits, eager_ops, backward_hits,
-// backward_misses, last step fully dispatched (0/1).
-int c3mlp_stats(c3mlp* m, int64_t* out7);
+// out[0..7] = steps, region_hits, single_op_hits, eager_ops, backward_hits,
+// backward_misses, last step fully dispatched (0/1), graph replays.
+int c3mlp_stats(c3mlp* m, int64_t* out8);
+// Capture one step as a HIP graph on `stream` (not NULL), then replay it.
+int c3mlp_capture(c3mlp* m, const void* X, const int32_t* labels, float lr, void* stream);
+int c3mlp_replay(c3mlp* m, void* stream);
 int c3mlp_set_keep_gradients(c3mlp* m, int keep);
 // Device pointer of a tensor of the last step: which = 0 activation(layer)
 // (layer 0..L), 1 outputGrad(layer), 2 weightGrad(layer), 3 biasGrad(layer).

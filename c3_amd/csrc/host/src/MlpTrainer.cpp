@@ -29,6 +29,10 @@ void check(int rc, const char* what) {
 
 Tensor devTensor(std::vector<size_t> shape, DType dt) { return Tensor(ShapeTag{}, std::move(shape), dt, DeviceType::kHIP); }
 
+void hipCheck(hipError_t e, const char* what) {
+    if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+
 }  // namespace
 
 MlpTrainer::MlpTrainer(std::vector<size_t> dims, size_t batch, DType dt) : dims_(std::move(dims)), batch_(batch), dt_(dt) {
@@ -66,7 +70,7 @@ Tensor MlpTrainer::layerForwardEager(size_t l, const Tensor& A, bool relu) {
     };
     if (dt_ == DType::kBFloat16) {
         // No bf16 single elementwise kernels: the layer runs as one eager Linear.
-        Tensor Y = devTensor({M, N}, dt_);
+        Tensor Y = make({M, N}, dt_);
         check(c3hip_linear_fwd(C3HIP_BF16, A.data(), W.data(), b.data_ptr<float>(), Y.data(), (int64_t)M, (int64_t)K,
                                (int64_t)N, relu ? C3HIP_ACT_RELU : C3HIP_ACT_NONE, st),
               "eager linear");
@@ -80,7 +84,7 @@ Tensor MlpTrainer::layerForwardEager(size_t l, const Tensor& A, bool relu) {
         T = *r;
         stats_.single_op_hits++;
     } else {
-        T = devTensor({M, N}, dt_);
+        T = make({M, N}, dt_);
         check(c3hip_matmul(C3HIP_F32, A.data(), W.data(), T.data(), (int64_t)M, (int64_t)K, (int64_t)N, 0, 0, st),
               "eager matmul");
         stats_.eager_ops++;
@@ -90,7 +94,7 @@ Tensor MlpTrainer::layerForwardEager(size_t l, const Tensor& A, bool relu) {
         Z = *r;
         stats_.single_op_hits++;
     } else {
-        Z = devTensor({M, N}, dt_);
+        Z = make({M, N}, dt_);
         check(c3hip_elementwise(C3HIP_EW_ADD, C3HIP_F32, T.data(), b.data(), 0.f, Z.data(), (int64_t)(M * N),
                                 (int64_t)N, st),
               "eager add");
@@ -105,7 +109,7 @@ Tensor MlpTrainer::layerForwardEager(size_t l, const Tensor& A, bool relu) {
         Y = *r;
         stats_.single_op_hits++;
     } else {
-        Y = devTensor({M, N}, dt_);
+        Y = make({M, N}, dt_);
         check(c3hip_elementwise(C3HIP_EW_RELU, C3HIP_F32, Z.data(), nullptr, 0.f, Y.data(), (int64_t)(M * N), 0, st),
               "eager relu");
         stats_.eager_ops++;
@@ -133,8 +137,8 @@ Tensor MlpTrainer::forward(const Tensor& X) {
             auto m = RF.matchFromPosition(prefix_, pos, A.shape(), {A.shape(), W_[l].shape()});
             if (m && m->len == layer_ops && m->kernel) {
                 try {
-                    acts_[l + 1] = C3KernelRegistry::getInstance().executeFusedWithInputs(m->kernel, {A, W_[l], b_[l]},
-                                                                                          KernelShapeInfo{});
+                    acts_[l + 1] = hold(C3KernelRegistry::getInstance().executeFusedWithInputs(
+                        m->kernel, {A, W_[l], b_[l]}, KernelShapeInfo{}));
                     done = acts_[l + 1].defined();
                 } catch (const std::exception& e) {
                     c3log(ErrorLevel::WARN, std::string("region kernel failed, running eagerly: ") + e.what());
@@ -157,8 +161,8 @@ float MlpTrainer::step(const Tensor& X, const void* labels, float lr, bool want_
     const size_t L = numLayers();
     const size_t C = dims_.back();
     Tensor logits = forward(X);
-    Tensor rows = devTensor({batch_}, DType::kFloat);
-    Tensor g = devTensor({batch_, C}, dt_);
+    Tensor rows = make({batch_}, DType::kFloat);
+    Tensor g = make({batch_, C}, dt_);
     check(c3hip_softmax_ce(hipDtype(dt_), logits.data(), static_cast<const int32_t*>(labels), rows.data_ptr<float>(),
                            g.data(), (int64_t)batch_, (int64_t)C, st),
           "softmax_ce");
@@ -180,16 +184,16 @@ float MlpTrainer::step(const Tensor& X, const void* labels, float lr, bool want_
         Tensor dA, dW, db;
         auto r = B.tryExecuteLinearBackward(g, {A, W_[i], Y}, relu);
         if (r && r->size() == 3) {
-            dA = (*r)[0];
-            dW = (*r)[1];
-            db = (*r)[2];
+            dA = hold((*r)[0]);
+            dW = hold((*r)[1]);
+            db = hold((*r)[2]);
             stats_.backward_hits++;
             step_bwd_hits_++;
         } else {
             const size_t M = A.shape()[0], K = dims_[i], N = dims_[i + 1];
-            dA = devTensor({M, K}, dt_);
-            dW = devTensor({K, N}, DType::kFloat);
-            db = devTensor({N}, DType::kFloat);
+            dA = make({M, K}, dt_);
+            dW = make({K, N}, DType::kFloat);
+            db = make({N}, DType::kFloat);
             check(c3hip_linear_bwd(hipDtype(dt_), A.data(), W_[i].data(), Y.data(), g.data(), dA.data(),
                                    dW.data_ptr<float>(), db.data_ptr<float>(), (int64_t)M, (int64_t)K, (int64_t)N,
                                    relu ? C3HIP_ACT_RELU : C3HIP_ACT_NONE, st),
@@ -212,13 +216,80 @@ float MlpTrainer::step(const Tensor& X, const void* labels, float lr, bool want_
     // model's threshold and stays unfused) and every backward fused.
     last_fully_dispatched_ = step_region_hits_ == L - 1 && step_bwd_hits_ == L;
     if (!want_loss) return std::nanf("");
-    Tensor sum = devTensor({1}, DType::kFloat);
+    Tensor sum = make({1}, DType::kFloat);
     check(c3hip_sum_reduce(rows.data_ptr<float>(), sum.data_ptr<float>(), 1, (int64_t)batch_, 1, st), "sum_reduce");
     float h = 0.f;
     if (hipMemcpyAsync(&h, sum.data(), 4, hipMemcpyDeviceToHost, (hipStream_t)st) != hipSuccess ||
         hipStreamSynchronize((hipStream_t)st) != hipSuccess)
         throw std::runtime_error("loss readback failed");
     return h / (float)batch_;
+}
+
+Tensor MlpTrainer::make(std::vector<size_t> shape, DType dt) { return hold(devTensor(std::move(shape), dt)); }
+
+Tensor MlpTrainer::hold(Tensor t) {
+    if (retain_ && t.defined()) retained_.push_back(t);
+    return t;
+}
+
+void MlpTrainer::captureStep(const Tensor& X, const void* labels, float lr) {
+    hipStream_t st = (hipStream_t)getCurrentStream();
+    if (st == nullptr) throw std::invalid_argument("MlpTrainer::captureStep: the default stream cannot be captured");
+    releaseGraph();
+    // One step with every buffer held grows the device pool to what a step
+    // needs with nothing freed, so the captured step allocates nothing new
+    // (no hipMalloc may run while the stream is capturing).
+    retain_ = true;
+    try {
+        step(X, labels, lr, false);
+        hipCheck(hipStreamSynchronize(st), "hipStreamSynchronize");
+        retained_.clear();
+        hipCheck(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+        try {
+            step(X, labels, lr, false);
+        } catch (...) {
+            hipGraph_t g = nullptr;
+            (void)hipStreamEndCapture(st, &g);
+            if (g) (void)hipGraphDestroy(g);
+            throw;
+        }
+        hipGraph_t g = nullptr;
+        hipCheck(hipStreamEndCapture(st, &g), "hipStreamEndCapture");
+        graph_ = g;
+        hipGraphExec_t ex = nullptr;
+        hipCheck(hipGraphInstantiate(&ex, g, nullptr, nullptr, 0), "hipGraphInstantiate");
+        graph_exec_ = ex;
+    } catch (...) {
+        retain_ = false;
+        retained_.clear();
+        releaseGraph();
+        throw;
+    }
+    // The captured step's buffers stay held for the graph's lifetime.
+    retain_ = false;
+    graph_dispatched_ = last_fully_dispatched_;
+}
+
+void MlpTrainer::replay() {
+    if (!graph_exec_) throw std::logic_error("MlpTrainer::replay: no captured step");
+    hipCheck(hipGraphLaunch((hipGraphExec_t)graph_exec_, (hipStream_t)getCurrentStream()), "hipGraphLaunch");
+    stats_.steps++;
+    stats_.graph_replays++;
+}
+
+void MlpTrainer::releaseGraph() {
+    if (graph_exec_) (void)hipGraphExecDestroy((hipGraphExec_t)graph_exec_);
+    if (graph_) (void)hipGraphDestroy((hipGraph_t)graph_);
+    graph_exec_ = nullptr;
+    graph_ = nullptr;
+    retained_.clear();
+}
+
+MlpTrainer::~MlpTrainer() {
+    if (graph_exec_ || graph_) {
+        (void)hipDeviceSynchronize();
+        releaseGraph();
+    }
 }
 
 size_t MlpTrainer::warmUp(const Tensor& X, const void* labels, float lr, size_t max_steps) {
@@ -350,6 +421,25 @@ int c3mlp_stats(c3mlp* m, int64_t* out) {
         out[4] = (int64_t)s.backward_hits;
         out[5] = (int64_t)s.backward_misses;
         out[6] = m->trainer.lastStepFullyDispatched() ? 1 : 0;
+        out[7] = (int64_t)s.graph_replays;
+    });
+}
+
+int c3mlp_capture(c3mlp* m, const void* X, const int32_t* labels, float lr, void* stream) {
+    return guarded([&] {
+        if (!m || !labels) throw std::invalid_argument("null argument");
+        if (!stream) throw std::invalid_argument("capture needs a non-default stream");
+        auto& t = m->trainer;
+        StreamScope ss(stream);
+        t.captureStep(borrow(X, {t.batch(), t.inFeatures()}, t.dtype(), "X"), labels, lr);
+    });
+}
+
+int c3mlp_replay(c3mlp* m, void* stream) {
+    return guarded([&] {
+        if (!m) throw std::invalid_argument("null trainer");
+        StreamScope ss(stream);
+        m->trainer.replay();
     });
 }
 

@@ -28,6 +28,8 @@ SIGNATURES = {
     "c3mlp_stats": (_int, [_vp, ctypes.POINTER(_i64)]),
     "c3mlp_set_keep_gradients": (_int, [_vp, _int]),
     "c3mlp_tensor": (_int, [_vp, _int, _int, ctypes.POINTER(_vp)]),
+    "c3mlp_capture": (_int, [_vp, _vp, _vp, _f, _vp]),
+    "c3mlp_replay": (_int, [_vp, _vp]),
 }
 
 _core = None
@@ -58,7 +60,7 @@ def _check(fn: str, rc: int) -> None:
 
 
 STAT_NAMES = ("steps", "region_hits", "single_op_hits", "eager_ops", "backward_hits", "backward_misses",
-              "fully_dispatched")
+              "fully_dispatched", "graph_replays")
 ACTIVATION, OUTPUT_GRAD, WEIGHT_GRAD, BIAS_GRAD = range(4)
 
 
@@ -110,9 +112,17 @@ class MlpTrainer:
         return n.value
 
     def stats(self) -> dict:
-        out = (_i64 * 7)()
+        out = (_i64 * 8)()
         _check("c3mlp_stats", load().c3mlp_stats(self._h, out))
         return dict(zip(STAT_NAMES, list(out)))
+
+    def capture(self, X: int, labels: int, lr: float, stream: int) -> None:
+        """Record one train step as a HIP graph on `stream` (not the default
+        stream); runs one real step first to size the device pool."""
+        _check("c3mlp_capture", load().c3mlp_capture(self._h, X, labels, lr, stream))
+
+    def replay(self, stream: int) -> None:
+        _check("c3mlp_replay", load().c3mlp_replay(self._h, stream))
 
     def keep_gradients(self, keep: bool = True) -> None:
         _check("c3mlp_set_keep_gradients", load().c3mlp_set_keep_gradients(self._h, int(keep)))

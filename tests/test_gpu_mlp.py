@@ -208,3 +208,36 @@ def test_trainer_rejects_bad_arguments(gpu, stream):
     with pytest.raises(T.TrainerError):
         tr.params(5)
     tr.close()
+
+
+def test_graph_replay_equals_eager_steps(gpu):
+    # A captured train step replayed N times leaves the parameters bit for bit
+    # where N eager steps do (same kernels, same launch shapes).
+    dims, batch, lr = [784, 256, 128, 10], 128, 0.05
+    X, Ws, bs, lbl = make_problem(dims, batch, 0xC5, N.F32)
+    side = torch.cuda.Stream()
+    s = side.cuda_stream
+    dXb, dl = dev(X), dev(lbl.astype(np.int32))
+    A = T.MlpTrainer(dims, batch, N.F32)
+    B = T.MlpTrainer(dims, batch, N.F32)
+    with torch.cuda.stream(side):
+        upload_params(A, Ws, bs, s)
+        upload_params(B, Ws, bs, s)
+        warm = A.warm_up(ptr(dXb), ptr(dl), lr, 16, s)
+        A.capture(ptr(dXb), ptr(dl), lr, s)       # one real step, then the recorded one
+        for _ in range(5):
+            A.replay(s)
+        for _ in range(warm + 1 + 5):
+            B.step(ptr(dXb), ptr(dl), lr, want_loss=False, stream=s)
+        side.synchronize()
+        for l in range(3):
+            for which in range(2):
+                pa, pb = A.params(l)[which], B.params(l)[which]
+                n = dims[l] * dims[l + 1] if which == 0 else dims[l + 1]
+                va, vb = fetch(pa, (n,), N.F32, s), fetch(pb, (n,), N.F32, s)
+                assert np.array_equal(va.view(np.int32), vb.view(np.int32)), (l, which)
+    assert A.stats()["graph_replays"] == 5
+    with pytest.raises(T.TrainerError, match="default stream"):
+        A.capture(ptr(dXb), ptr(dl), lr, 0)
+    A.close()
+    B.close()
