@@ -165,6 +165,7 @@ def main():
         out["bf16_sweep"] = bench_bf16_sweep(torch, C, dev, s)
         out["elementwise"] = {"2^28": bench_elementwise(torch, C, dev, s, 1 << 28, sets=1),
                               "2^24": bench_elementwise(torch, C, dev, s, 1 << 24, sets=8)}
+        out["backward_chain"] = bench_backward_chain(torch, C, dev, s)
         out["mlp_784_256_128_10_fp32"] = bench_mlp(torch, C, dev, s, [784, 256, 128, 10], 128, C.F32,
                                                    steps=200, uniform_x=True, graph=True)
         out["mlp_deep_bf16"] = bench_mlp(torch, C, dev, s, [4096, 8192, 8192, 8192, 4096, 1000], 16384, C.BF16,
@@ -252,6 +253,60 @@ def bench_elementwise(torch, C, dev, s, n, sets, iters=10):
     del bufs
     torch.cuda.empty_cache()
     return {"n": n, "operand_sets": sets, "ops": res}
+
+
+def bench_backward_chain(torch, C, dev, s, n=1 << 26, iters=10):
+    """Fused backward chains over n fp32 elements against the same nodes run one
+    by one.  Algorithmic bytes of a w-node chain: 4 * (1 + 2w) per element
+    (grad and w forward inputs read, w upstream grads written); one by one the
+    nodes move 4 * 3w (Neg: 8 B per element)."""
+    chains = {"ReLU+Sigmoid": [C.CHAIN_RELU, C.CHAIN_SIGMOID], "Sigmoid+Tanh": [C.CHAIN_SIGMOID, C.CHAIN_TANH],
+              "ReLU+Log+Neg+Exp": [C.CHAIN_RELU, C.CHAIN_LOG, C.CHAIN_NEG, C.CHAIN_EXP]}
+    single = {C.CHAIN_RELU: (C.EW_RELU_BWD, True), C.CHAIN_SIGMOID: (C.EW_SIGMOID_BWD, True),
+              C.CHAIN_TANH: (C.EW_TANH_BWD, True), C.CHAIN_EXP: (C.EW_EXP_BWD, True),
+              C.CHAIN_LOG: (C.EW_DIV, False), C.CHAIN_NEG: (C.EW_NEG, False)}
+    g = torch.randn(n, device=dev)
+    xs = [torch.rand(n, device=dev) * 4.0 + 0.25 for _ in range(4)]
+    outs = [torch.empty(n, device=dev) for _ in range(4)]
+
+    def timed(fn):
+        fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(iters):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / iters
+
+    res = {}
+    for name, nodes in chains.items():
+        w = len(nodes)
+
+        def fused():
+            C.backward_chain(C.F32, g.data_ptr(), [x.data_ptr() for x in xs[:w]], nodes,
+                             [o.data_ptr() for o in outs[:w]], n, s)
+
+        def one_by_one():
+            cur = g
+            for k, node in enumerate(nodes):
+                op, x_first = single[node]
+                if node == C.CHAIN_NEG:
+                    C.elementwise(op, C.F32, cur.data_ptr(), None, 0.0, outs[k].data_ptr(), n, 0, s)
+                elif x_first:
+                    C.elementwise(op, C.F32, xs[k].data_ptr(), cur.data_ptr(), 0.0, outs[k].data_ptr(), n, 0, s)
+                else:
+                    C.elementwise(op, C.F32, cur.data_ptr(), xs[k].data_ptr(), 0.0, outs[k].data_ptr(), n, 0, s)
+                cur = outs[k]
+
+        ms_f, ms_u = timed(fused), timed(one_by_one)
+        gbs = 4.0 * (1 + 2 * w) * n / (ms_f * 1e-3) / 1e9
+        res[name] = {"fused_ms": round(ms_f, 4), "one_by_one_ms": round(ms_u, 4), "speedup": round(ms_u / ms_f, 3),
+                     "fused_GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
+    del g, xs, outs
+    torch.cuda.empty_cache()
+    return {"n": n, "chains": res}
 
 
 SWEEP = [(m, k, n) for m in (1024, 4096, 16384) for k in (1024, 4096, 8192) for n in (1024, 4096, 8192)]

@@ -74,7 +74,9 @@ enum class KernelKind {
     SumReduce,     // Add node backward, input 1 (bias): column sums of grad
     MatMulBackwardA, // MatMul node backward, input 0: grad . B^T, inputs [grad, B]
     MatMulBackwardB, // MatMul node backward, input 1: A^T . grad, inputs [grad, A]
-    LinearBwd      // fused layer backward: inputs [dY, X, W, Y] -> [dX, dW, db]
+    LinearBwd,     // fused layer backward: inputs [dY, X, W, Y] -> [dX, dW, db]
+    BackwardChain  // fused backward of single-input nodes: inputs [grad, x_0..x_{w-1}] ->
+                   // [g_1..g_w], the upstream grad of each node (c3hip_backward_chain)
 };
 
 struct KernelSpec {
@@ -85,6 +87,7 @@ struct KernelSpec {
     int act = 0;                                  // C3HIP_ACT_* for LinearFwd / LinearBwd
     bool transA = false, transB = false;          // MatMul
     int axis = 0;                                 // SumReduce
+    std::vector<int> chain;                       // C3HIP_CHAIN_* per node, BackwardChain
     std::vector<std::vector<size_t>> input_shapes;
     std::vector<size_t> out_shape;
     DType dtype = DType::kFloat;

@@ -28,6 +28,7 @@ const char* kindName(KernelKind k) {
         case KernelKind::MatMulBackwardA: return "matmul_bwd_a";
         case KernelKind::MatMulBackwardB: return "matmul_bwd_b";
         case KernelKind::LinearBwd: return "linear_bwd";
+        case KernelKind::BackwardChain: return "bwd_chain";
     }
     return "?";
 }
@@ -71,7 +72,12 @@ std::string KernelSpec::toString() const {
     std::ostringstream ss;
     ss << "rh=" << std::hex << RollingHash::hashSequence(op_seq) << std::dec << "|kind=" << kindName(kind)
        << "|ew=" << ew_op << "|alpha=" << alpha << "|act=" << act << "|t=" << transA << transB << "|axis=" << axis
-       << "|dtype=" << static_cast<int>(dtype) << "|in=";
+       << "|dtype=" << static_cast<int>(dtype);
+    if (!chain.empty()) {
+        ss << "|chain=";
+        for (int c : chain) ss << c << ",";
+    }
+    ss << "|in=";
     for (const auto& s : input_shapes) ss << shapeToString(s) << ";";
     ss << "|out=" << shapeToString(out_shape);
     return ss.str();
@@ -82,7 +88,8 @@ std::string KernelSpec::moduleName() const {
         case KernelKind::Elementwise:
         case KernelKind::ReLUBackward:
         case KernelKind::UnaryBackward:
-        case KernelKind::DivBackwardB: return "elementwise";
+        case KernelKind::DivBackwardB:
+        case KernelKind::BackwardChain: return "elementwise";
         case KernelKind::SumReduce: return "reduce";
         case KernelKind::AddBackwardLhs: return "";
         default: return dtype == DType::kBFloat16 ? "gemm_bf16" : "gemm_f32";

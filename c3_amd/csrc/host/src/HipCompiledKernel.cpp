@@ -197,6 +197,29 @@ std::vector<Tensor> HipCompiledKernel::execute(const std::vector<Tensor>& in) {
                   "c3hip_linear_bwd");
             return {dX, dW, db};
         }
+        case KernelKind::BackwardChain: {
+            // [grad, x_0..x_{w-1}] -> [g_1..g_w], every tensor of grad's shape.
+            const size_t w = s.chain.size();
+            if (w == 0 || w > C3HIP_CHAIN_MAX_NODES) throw std::runtime_error("backward chain: bad node count");
+            need(1 + w);
+            const Tensor& g = in[0];
+            std::vector<const void*> xs(w);
+            std::vector<void*> outs(w);
+            std::vector<Tensor> res;
+            res.reserve(w);
+            for (size_t k = 0; k < w; ++k) {
+                const Tensor& x = in[1 + k];
+                if (x.shape() != g.shape() || x.dtype() != DType::kFloat || g.dtype() != DType::kFloat)
+                    throw std::runtime_error("backward chain: inputs differ in shape from grad or are not fp32");
+                xs[k] = x.data();
+                res.emplace_back(ShapeTag{}, g.shape(), DType::kFloat, DeviceType::kHIP);
+                outs[k] = res.back().data();
+            }
+            check(c3hip_backward_chain(C3HIP_F32, g.data(), xs.data(), s.chain.data(), (int)w, outs.data(),
+                                       (int64_t)g.numel(), st),
+                  "c3hip_backward_chain");
+            return res;
+        }
     }
     throw std::runtime_error("HipCompiledKernel: unknown kernel kind");
 }

@@ -145,6 +145,75 @@ C3_EW(sigmoid_bwd, EW_SIGMOID_BWD)
 C3_EW(tanh_bwd, EW_TANH_BWD)
 C3_EW(exp_bwd, EW_EXP_BWD)
 
+// ---- fused backward chain of single-input nodes ----------------------------
+// g_0 = grad; node k (k = 0 most downstream) maps g_k to g_{k+1} with its
+// per-node rule from its forward input x_k, and out_k = g_{k+1} is stored (the
+// upstream grad of every node, as the reference's multi-output fused graph
+// returns them: src/C3/C3BackwardCapture.cpp:1140-1210).  Each rule is the
+// same ew_apply step as the single-node kernel, so the chain is bit-identical
+// to running the nodes one by one; only the intermediate re-reads go away.
+enum { CH_RELU = 0, CH_SIGMOID = 1, CH_TANH = 2, CH_EXP = 3, CH_LOG = 4, CH_NEG = 5 };
+constexpr int kChainMax = 4;
+
+struct ChainArgs {
+    const float* g;
+    const float* x[kChainMax];  // x[k] unused (may be null) for a Neg node
+    float* out[kChainMax];      // null: g_{k+1} is not stored
+    int node[kChainMax];
+    int w;
+    int64_t n;                  // elements (vector kernel: the count of float4)
+};
+
+__device__ __forceinline__ float chain_step(int node, float g, float x) {
+    switch (node) {
+        case CH_RELU: return ew_apply<EW_RELU_BWD>(x, g, 0.0f);
+        case CH_SIGMOID: return ew_apply<EW_SIGMOID_BWD>(x, g, 0.0f);
+        case CH_TANH: return ew_apply<EW_TANH_BWD>(x, g, 0.0f);
+        case CH_EXP: return ew_apply<EW_EXP_BWD>(x, g, 0.0f);
+        case CH_LOG: return ew_apply<EW_DIV>(g, x, 0.0f);
+        default: return ew_apply<EW_NEG>(g, 0.0f, 0.0f);
+    }
+}
+
+// One float4 per thread.  Every load of the element is issued before the
+// first store, so an output may alias an input at the same offsets.
+extern "C" __global__ __launch_bounds__(kThreads) void c3_bwd_chain_f32_v(ChainArgs p) {
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i >= p.n) return;
+    f32x4 g = ld_nt((const f32x4*)p.g + i);
+    f32x4 x[kChainMax];
+#pragma unroll
+    for (int k = 0; k < kChainMax; ++k)
+        if (k < p.w && p.node[k] != CH_NEG) x[k] = ld_nt((const f32x4*)p.x[k] + i);
+#pragma unroll
+    for (int k = 0; k < kChainMax; ++k) {
+        if (k < p.w) {
+            const int node = p.node[k];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) g[e] = chain_step(node, g[e], node == CH_NEG ? 0.0f : x[k][e]);
+            if (p.out[k]) st_nt(g, (f32x4*)p.out[k] + i);
+        }
+    }
+}
+
+// Any n and alignment: grid-stride over elements.
+extern "C" __global__ __launch_bounds__(kThreads) void c3_bwd_chain_f32_s(ChainArgs p) {
+    const int64_t stride = (int64_t)gridDim.x * kThreads;
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < p.n; i += stride) {
+        float g = p.g[i];
+        float x[kChainMax];
+#pragma unroll
+        for (int k = 0; k < kChainMax; ++k) x[k] = (k < p.w && p.node[k] != CH_NEG) ? p.x[k][i] : 0.0f;
+#pragma unroll
+        for (int k = 0; k < kChainMax; ++k) {
+            if (k < p.w) {
+                g = chain_step(p.node[k], g, x[k]);
+                if (p.out[k]) p.out[k][i] = g;
+            }
+        }
+    }
+}
+
 // Three-input ops: out = op(a, b, c), no broadcast, any n and alignment.
 extern "C" __global__ __launch_bounds__(kThreads) void c3_ew3_div_bwd_b_f32(const float* __restrict__ a,
                                                                           const float* __restrict__ b,

@@ -40,6 +40,18 @@ struct GemmArgs {
     int _pad;
 };
 
+// Kernel argument block of the fused backward chain (mirrors ChainArgs in
+// c3_amd/csrc/kernels/elementwise.hip).
+constexpr int kChainMaxNodes = 4;
+struct ChainArgs {
+    const float* g;
+    const float* x[kChainMaxNodes];
+    float* out[kChainMaxNodes];
+    int node[kChainMaxNodes];
+    int w;
+    int64_t n;
+};
+
 inline bool aligned16(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace c3hip

@@ -347,6 +347,44 @@ int c3hip_elementwise3(int op, int dtype, const void* a, const void* b, const vo
     return launch("c3_ew3_div_bwd_b_f32", dim3((unsigned)blocks), dim3(256), args, (hipStream_t)stream);
 }
 
+int c3hip_backward_chain(int dtype, const void* grad, const void* const* x, const int* nodes, int num_nodes,
+                         void* const* outs, int64_t n, void* stream) {
+    clear_error();
+    int rc = check_dtype(dtype);
+    if (rc) return rc;
+    if (dtype != C3HIP_F32) return set_error(C3HIP_ERR_UNSUPPORTED, "backward chains take fp32 only");
+    if (num_nodes < 1 || num_nodes > kChainMaxNodes)
+        return set_error(C3HIP_ERR_INVALID, "num_nodes must be 1.." + std::to_string(kChainMaxNodes));
+    if (!nodes) return set_error(C3HIP_ERR_INVALID, "null node list");
+    for (int k = 0; k < num_nodes; ++k)
+        if (nodes[k] < C3HIP_CHAIN_RELU || nodes[k] > C3HIP_CHAIN_NEG)
+            return set_error(C3HIP_ERR_INVALID, "unknown chain node " + std::to_string(nodes[k]));
+    if (n < 0) return set_error(C3HIP_ERR_INVALID, "n < 0");
+    if (n == 0) return C3HIP_OK;
+    if (!grad || !x || !outs) return set_error(C3HIP_ERR_INVALID, "null pointer");
+    ChainArgs p{};
+    p.g = static_cast<const float*>(grad);
+    p.w = num_nodes;
+    bool vec = n % 4 == 0 && aligned16(grad);
+    for (int k = 0; k < num_nodes; ++k) {
+        if (nodes[k] != C3HIP_CHAIN_NEG && !x[k]) return set_error(C3HIP_ERR_INVALID, "null forward input");
+        p.node[k] = nodes[k];
+        p.x[k] = nodes[k] == C3HIP_CHAIN_NEG ? nullptr : static_cast<const float*>(x[k]);
+        p.out[k] = static_cast<float*>(outs[k]);
+        vec = vec && aligned16(p.x[k]) && aligned16(p.out[k]);
+    }
+    void* args[] = {&p};
+    if (vec) {
+        p.n = n / 4;
+        const int64_t blocks = (p.n + 255) / 256;  // one float4 per thread
+        if (blocks > 0x7fffffff) return set_error(C3HIP_ERR_TOO_LARGE, "chain grid too large");
+        return launch("c3_bwd_chain_f32_v", dim3((unsigned)blocks), dim3(256), args, (hipStream_t)stream);
+    }
+    p.n = n;
+    const int64_t blocks = std::min<int64_t>((n + 255) / 256, 1 << 16);
+    return launch("c3_bwd_chain_f32_s", dim3((unsigned)blocks), dim3(256), args, (hipStream_t)stream);
+}
+
 int c3hip_matmul(int dtype, const void* A, const void* B, void* C, int64_t M, int64_t K, int64_t N, int transA,
                  int transB, void* stream) {
     clear_error();

@@ -23,6 +23,11 @@ ACT_NONE, ACT_RELU, ACT_SIGMOID, ACT_TANH = 0, 1, 2, 3
 EW_ADD, EW_SUB, EW_MUL, EW_DIV, EW_RELU, EW_RELU_BWD, EW_NEG, EW_SCALE = range(8)
 EW_SIGMOID, EW_TANH, EW_EXP, EW_LOG, EW_SIGMOID_BWD, EW_TANH_BWD, EW_EXP_BWD = range(8, 15)
 EW3_DIV_BWD_B = 0
+CHAIN_RELU, CHAIN_SIGMOID, CHAIN_TANH, CHAIN_EXP, CHAIN_LOG, CHAIN_NEG = range(6)
+CHAIN_MAX_NODES = 4
+# Node type names of the backward chain (the host framework's node types).
+CHAIN_NODES = {"ReLU": CHAIN_RELU, "Sigmoid": CHAIN_SIGMOID, "Tanh": CHAIN_TANH, "Exp": CHAIN_EXP,
+               "Log": CHAIN_LOG, "Neg": CHAIN_NEG}
 # The eight single-node ops of the fused path's elementwise set.
 EW_OPS = {"add": EW_ADD, "sub": EW_SUB, "mul": EW_MUL, "div": EW_DIV, "relu": EW_RELU,
           "relu_bwd": EW_RELU_BWD, "neg": EW_NEG, "scale": EW_SCALE}
@@ -41,6 +46,8 @@ SIGNATURES = {
     "c3hip_code_object_path": (_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_size_t]),
     "c3hip_elementwise": (_int, [_int, _int, _vp, _vp, _f, _vp, _i64, _i64, _vp]),
     "c3hip_elementwise3": (_int, [_int, _int, _vp, _vp, _vp, _vp, _i64, _vp]),
+    "c3hip_backward_chain": (_int, [_int, _vp, ctypes.POINTER(_vp), ctypes.POINTER(_int), _int,
+                                    ctypes.POINTER(_vp), _i64, _vp]),
     "c3hip_matmul": (_int, [_int, _vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _vp]),
     "c3hip_linear_fwd": (_int, [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _vp]),
     "c3hip_linear_bwd": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _vp]),
@@ -109,6 +116,17 @@ def elementwise(op: int, dtype: int, a: int, b: int | None, alpha: float, out: i
 
 def elementwise3(op: int, dtype: int, a: int, b: int, c: int, out: int, n: int, stream: int = 0) -> None:
     _check("c3hip_elementwise3", load().c3hip_elementwise3(op, dtype, a, b, c, out, n, stream))
+
+
+def backward_chain(dtype: int, grad: int, xs, nodes, outs, n: int, stream: int = 0) -> None:
+    """Fused backward of len(nodes) single-input nodes (node 0 downstream);
+    xs[k] is node k's forward input (None for Neg), outs[k] its upstream grad
+    (None: not stored)."""
+    w = len(nodes)
+    xa = (_vp * max(w, 1))(*[x or None for x in xs])
+    oa = (_vp * max(w, 1))(*[o or None for o in outs])
+    na = (_int * max(w, 1))(*nodes)
+    _check("c3hip_backward_chain", load().c3hip_backward_chain(dtype, grad, xa, na, w, oa, n, stream))
 
 
 def matmul(dtype: int, A: int, B: int, C: int, M: int, K: int, N: int, transA: bool = False,

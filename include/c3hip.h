@@ -69,6 +69,16 @@ extern "C" {
 #define C3HIP_EW3_DIV_BWD_B 0   /* -((a / (b * b)) * c): Div's gradient for its divisor,
                                    a = dividend, b = divisor, c = grad (buildDivBackwardGraph) */
 
+/* Node types of a fused backward chain (c3hip_backward_chain): the rule maps
+ * the node's downstream grad g to its upstream grad from its forward input x. */
+#define C3HIP_CHAIN_RELU 0     /* (x > 0 ? 1 : 0) * g                  (src/C3/C3BackwardCapture.cpp:501-528) */
+#define C3HIP_CHAIN_SIGMOID 1  /* s = 1/(1+expf(-x)); g * (s * (1 - s))           (:530-567) */
+#define C3HIP_CHAIN_TANH 2     /* t = (e^x - e^-x)/(e^x + e^-x); g * (1 - t*t)     (:569-616) */
+#define C3HIP_CHAIN_EXP 3      /* expf(x) * g                                      (:823-849) */
+#define C3HIP_CHAIN_LOG 4      /* g / x                                            (:851-872) */
+#define C3HIP_CHAIN_NEG 5      /* -g; x unused (may be NULL)                       (:725-741) */
+#define C3HIP_CHAIN_MAX_NODES 4 /* kFusionWindowSize, include/C3/C3BackwardCapture.h:390 */
+
 /* ABI version of the loaded library (C3HIP_ABI_VERSION). */
 int c3hip_abi_version(void);
 
@@ -131,6 +141,22 @@ int c3hip_elementwise(int op, int dtype, const void* a, const void* b, float alp
  */
 int c3hip_elementwise3(int op, int dtype, const void* a, const void* b, const void* c, void* out, int64_t n,
                        void* stream);
+
+/*
+ * Fused backward of a chain of num_nodes (1..C3HIP_CHAIN_MAX_NODES)
+ * single-input elementwise nodes over n contiguous elements, node 0 the most
+ * downstream: g_0 = grad, g_{k+1} = rule(nodes[k], g_k, x[k]) and
+ * outs[k] = g_{k+1} (the upstream grad of node k; a NULL outs[k] is not
+ * stored).  Every rule is evaluated with the same IEEE operations as the
+ * single-node backward kernels, so the outputs are bit-identical to running
+ * the nodes one by one.  An output may alias an input at the same offsets.
+ * dtype: C3HIP_F32.  Replaces the multi-output fused graph that
+ * C3BackwardCapture::compileFusedBackwardAsync builds by merging the nodes'
+ * backward graphs (src/C3/C3BackwardCapture.cpp:1140-1210) and the kernel
+ * tryExecuteFusedBackward runs (:1344-1637).
+ */
+int c3hip_backward_chain(int dtype, const void* grad, const void* const* x, const int* nodes, int num_nodes,
+                         void* const* outs, int64_t n, void* stream);
 
 /*
  * C[M,N] = op(A) . op(B), fp32 accumulation.  transA != 0: A is stored

@@ -185,6 +185,32 @@ def elementwise3(op, a, b, c):
     return out
 
 
+CHAIN_RELU, CHAIN_SIGMOID, CHAIN_TANH, CHAIN_EXP, CHAIN_LOG, CHAIN_NEG = range(6)
+
+
+def backward_chain(nodes, grad, xs):
+    """Upstream grads of a chain of single-input nodes, node 0 downstream:
+    g_0 = grad, g_{k+1} = rule_k(g_k, x_k); returns [g_1, ..., g_w].
+
+    The reference merges each node's own backward graph into one
+    multi-output graph, feeding node k's output grad to node k+1
+    (src/C3/C3BackwardCapture.cpp:1140-1210), so each step is that node's
+    rule: ReLU Gt+Mul (:501-528), Sigmoid (:530-567), Tanh (:569-616),
+    Exp (:823-849), Log grad/x (:851-872), Neg -grad (:725-741)."""
+    rule = {CHAIN_RELU: lambda g, x: elementwise(EW_RELU_BWD, x, g),
+            CHAIN_SIGMOID: lambda g, x: elementwise(EW_SIGMOID_BWD, x, g),
+            CHAIN_TANH: lambda g, x: elementwise(EW_TANH_BWD, x, g),
+            CHAIN_EXP: lambda g, x: elementwise(EW_EXP_BWD, x, g),
+            CHAIN_LOG: lambda g, x: elementwise(EW_DIV, g, x),
+            CHAIN_NEG: lambda g, x: elementwise(EW_NEG, g)}
+    g = _c(grad).reshape(-1)
+    outs = []
+    for node, x in zip(nodes, xs):
+        g = rule[node](g, None if x is None else _c(x).reshape(-1))
+        outs.append(g)
+    return outs
+
+
 def act_grad(y, g, act):
     y, g = _c(y), _c(g)
     out = np.empty_like(y)

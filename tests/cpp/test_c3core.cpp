@@ -68,6 +68,7 @@ public:
                         case C3HIP_EW_ADD: y[i] = x + r; break;
                         case C3HIP_EW_SUB: y[i] = x - r; break;
                         case C3HIP_EW_MUL: y[i] = x * r; break;
+                        case C3HIP_EW_DIV: y[i] = x / r; break;
                         case C3HIP_EW_RELU: y[i] = x > 0 ? x : 0.f; break;
                         case C3HIP_EW_NEG: y[i] = -x; break;
                         default: throw std::runtime_error("op");
@@ -82,6 +83,24 @@ public:
                 return {o};
             }
             case KernelKind::AddBackwardLhs: return {in[0]};
+            case KernelKind::BackwardChain: {
+                // [grad, x_0..] -> [g_1..]: the exact rules (relu mask, log g/x, neg).
+                std::vector<Tensor> outs;
+                std::vector<float> g = vals(in[0]);
+                for (size_t k = 0; k < s_.chain.size(); ++k) {
+                    const float* x = in[1 + k].data_ptr<float>();
+                    for (size_t i = 0; i < g.size(); ++i) {
+                        switch (s_.chain[k]) {
+                            case C3HIP_CHAIN_RELU: g[i] = (x[i] > 0 ? 1.f : 0.f) * g[i]; break;
+                            case C3HIP_CHAIN_LOG: g[i] = g[i] / x[i]; break;
+                            case C3HIP_CHAIN_NEG: g[i] = -g[i]; break;
+                            default: throw std::runtime_error("HostKernel: chain node not implemented");
+                        }
+                    }
+                    outs.push_back(host(in[0].shape(), g));
+                }
+                return outs;
+            }
             case KernelKind::SumReduce: {
                 const size_t M = in[0].shape()[0], N = in[0].shape()[1];
                 Tensor o(ShapeTag{}, {N}, DType::kFloat, DeviceType::kCPU);
@@ -672,6 +691,146 @@ TEST(backward_capture_rules_and_keys) {
     CHECK(!B.tryExecuteBackward("Softmax", g, {x}).has_value());
     const auto st = B.getStats();
     CHECK(st.cache_hit_count == 3 && st.cache_miss_count == 3 && st.compiles_submitted == 5);
+}
+
+// ------------------------------------------------- fused backward chains --
+namespace {
+// A host-framework autograd node: its type, upstream links and forward inputs.
+struct FakeNode : BackwardNode {
+    FakeNode(std::string t, std::vector<Tensor> in) : type(std::move(t)), inputs(std::move(in)) {}
+    std::string typeName() const override { return type; }
+    std::vector<std::shared_ptr<BackwardNode>> getUpStreamNodes() const override { return ups; }
+    std::vector<Tensor> getInputs() const override { return inputs; }
+    std::string type;
+    std::vector<Tensor> inputs;
+    std::vector<std::shared_ptr<BackwardNode>> ups;
+};
+
+std::shared_ptr<FakeNode> node(std::string t, std::vector<Tensor> in, std::shared_ptr<BackwardNode> up) {
+    auto n = std::make_shared<FakeNode>(std::move(t), std::move(in));
+    if (up) n->ups.push_back(std::move(up));
+    return n;
+}
+}  // namespace
+
+TEST(backward_chain_keys_and_window) {
+    HostBackend hb;
+    using B = C3BackwardCapture;
+    CHECK_EQ(B::makeSequenceKey({"ReLU", "Sigmoid"}), std::string("ReLU+Sigmoid"));
+    CHECK_EQ(B::makeSequenceKey({"LReLU", "GELU", "Tanh"}), std::string("Other+Other+Tanh"));
+    CHECK_EQ(B::makeFusedBackwardKey("ReLU+Sigmoid", {32, 64}, {32, 64}),
+             std::string("backward_fused_ReLU+Sigmoid|g:32,64,|i:32,64,"));
+    CHECK(!B::isFusableSequence({"ReLU"}));
+    CHECK(!B::isFusableSequence({"ReLU", "Add"}));
+    CHECK(B::isFusableSequence({"ReLU", "Sin", "Neg"}));
+    KernelSpec sp;
+    const std::vector<size_t> g = {4, 6};
+    CHECK(B::buildChainSpec({"ReLU", "Log", "Neg"}, {g, g, g}, {g, g, g}, DType::kFloat, &sp));
+    CHECK(sp.kind == KernelKind::BackwardChain &&
+          sp.chain == (std::vector<int>{C3HIP_CHAIN_RELU, C3HIP_CHAIN_LOG, C3HIP_CHAIN_NEG}) &&
+          sp.input_shapes.size() == 4 && sp.out_shape == g && sp.moduleName() == "elementwise");
+    CHECK(!B::buildChainSpec({"ReLU", "GELU"}, {g, g}, {g, g}, DType::kFloat, &sp));       // no rule
+    CHECK(!B::buildChainSpec({"ReLU", "Log"}, {g, g}, {g, {6}}, DType::kFloat, &sp));       // shapes differ
+    CHECK(!B::buildChainSpec({"ReLU", "Log"}, {g, g}, {g, g}, DType::kBFloat16, &sp));      // fp32 only
+    CHECK(!B::buildChainSpec({"ReLU", "Log", "Neg", "Exp", "Tanh"}, std::vector<std::vector<size_t>>(5, g),
+                             std::vector<std::vector<size_t>>(5, g), DType::kFloat, &sp));  // > window
+    // The window: a pair compiles on its first sighting, then the window restarts.
+    auto& C = B::getInstance();
+    Tensor x = host(g, std::vector<float>(24, 1.f));
+    C.recordBackwardNode("Add", g, g, {x});  // not a chain node: ignored
+    C.recordBackwardNode("ReLU", g, g, {x});
+    C.recordBackwardNode("Log", g, g, {x});
+    C.waitForPendingCompiles();
+    CHECK(C3KernelRegistry::getInstance().hasBackwardKey("backward_fused_ReLU+Log|g:4,6,|i:4,6,"));
+    C.recordBackwardNode("Neg", g, g, {x});  // counts ReLU+Log again, restarts at [Neg]
+    std::vector<std::string> tail;
+    CHECK(C.getLatestSequenceTail(tail, 1) && tail == std::vector<std::string>{"Neg"});
+    CHECK(!C.getLatestSequenceTail(tail, 2));
+    C.recordBackwardNode("ReLU", g, g, {x});
+    C.waitForPendingCompiles();
+    CHECK(C3KernelRegistry::getInstance().hasBackwardKey("backward_fused_Neg+ReLU|g:4,6,|i:4,6,"));
+    std::string key;
+    Tensor gt = host(g, std::vector<float>(24, 0.f));
+    CHECK(C.tryLookupFusedBackwardKey(gt, g, key) && key == "backward_fused_Neg+ReLU|g:4,6,|i:4,6,");
+    // Mixed grad shapes along a pair: counted (the tail windows do not check
+    // shapes) but never compiled; a GELU pair has no rule.
+    C.clearCallScopedState();
+    C.recordBackwardNode("ReLU", g, g, {x});
+    C.recordBackwardNode("Log", {24}, {24}, {x});
+    C.clearCallScopedState();
+    C.recordBackwardNode("GELU", g, g, {x});
+    C.recordBackwardNode("ReLU", g, g, {x});
+    C.waitForPendingCompiles();
+    const auto st = C.getStats();
+    CHECK(st.fusion_compile_count == 2);
+    CHECK(!C3KernelRegistry::getInstance().hasBackwardKey("backward_fused_ReLU+Log|g:4,6,|i:24,"));
+    CHECK(!C3KernelRegistry::getInstance().hasBackwardKey("backward_fused_Other+ReLU|g:4,6,|i:4,6,"));
+}
+
+// y = relu(wrap(log(x2))): backward runs ReLU (N0), then Log (N1).  The first
+// pass runs the nodes one by one and records them; the chain compiles; the
+// second pass runs it once at N0 and hands N1 its grad from the intercept map.
+TEST(backward_chain_fused_execution) {
+    HostBackend hb;
+    auto& C = C3BackwardCapture::getInstance();
+    const std::vector<size_t> s = {2, 3};
+    Tensor x2 = host(s, {0.5f, 2.f, 4.f, 8.f, 0.25f, 1.f});
+    Tensor x1 = host(s, {-1.f, 0.f, 2.f, 3.f, -0.5f, 7.f});  // the ReLU's input (log's output, say)
+    Tensor gy = host(s, {1.f, 2.f, 3.f, -4.f, 5.f, -6.f});
+    auto leaf = node("AccumulateGrad", {}, nullptr);
+    auto nlog = node("Log", {x2}, leaf);
+    auto wrap = node("Factor", {x1}, nlog);
+    auto nrelu = node("ReLU", {x1}, wrap);
+    const std::vector<float> want1 = {0.f, 0.f, 3.f, -4.f, 0.f, -6.f};               // (x1 > 0) * gy
+    const std::vector<float> want2 = {0.f, 0.f, 0.75f, -0.5f, 0.f, -6.f};            // want1 / x2
+    // Pass 1: nothing compiled yet.
+    CHECK(!C.tryExecuteBackward(nrelu.get(), gy, {x1}).has_value());
+    C.recordBackwardNode("ReLU", s, s, {x1});
+    Tensor g1 = host(s, want1);
+    CHECK(!C.tryExecuteBackward(nlog.get(), g1, {x2}).has_value());
+    C.recordBackwardNode("Log", s, s, {x2});
+    C.clearCallScopedState();
+    C.waitForPendingCompiles();
+    // Pass 2: one chain launch serves both nodes.
+    auto r0 = C.tryExecuteBackward(nrelu.get(), gy, {x1});
+    CHECK(r0.has_value() && r0->size() == 1 && vals((*r0)[0]) == want1);
+    auto r1 = C.tryExecuteBackward(nlog.get(), (*r0)[0], {x2});
+    CHECK(r1.has_value() && vals((*r1)[0]) == want2);
+    auto st = C.getStats();
+    CHECK(st.fusion_hit_count == 2);
+    // The intercepted grad is consumed once: a third call runs the Log node's
+    // own kernel (compiled in pass 1) from the grad it is given.
+    auto r2 = C.tryExecuteBackward(nlog.get(), (*r0)[0], {x2});
+    CHECK(r2.has_value() && vals((*r2)[0]) == want2);
+    CHECK(C.getStats().fusion_hit_count == 2);
+    C.clearCallScopedState();
+    // Four wrappers between the nodes: beyond the skip bound, no chain.
+    auto w4 = node("Factor", {x1}, node("Factor", {x1}, node("Factor", {x1}, node("Factor", {x1}, nlog))));
+    auto far = node("ReLU", {x1}, w4);
+    const size_t misses = C.getStats().fusion_miss_count;
+    auto rf = C.tryExecuteBackward(far.get(), gy, {x1});
+    CHECK(rf.has_value() && vals((*rf)[0]) == want1);  // the ReLU node's own kernel
+    CHECK(C.getStats().fusion_miss_count == misses + 1);
+    CHECK(C.getStats().fusion_hit_count == 2);
+    // Three wrappers: within the bound, the chain runs.
+    auto w3 = node("Factor", {x1}, node("Factor", {x1}, node("Factor", {x1}, nlog)));
+    auto near = node("ReLU", {x1}, w3);
+    auto rn = C.tryExecuteBackward(near.get(), gy, {x1});
+    CHECK(rn.has_value() && vals((*rn)[0]) == want1 && C.getStats().fusion_hit_count == 3);
+    C.clearCallScopedState();
+    // An upstream node whose input has another shape ends the chain.
+    Tensor x2b = host({6}, {0.5f, 2.f, 4.f, 8.f, 0.25f, 1.f});
+    auto nlogb = node("Log", {x2b}, leaf);
+    auto nrelub = node("ReLU", {x1}, nlogb);
+    const size_t hits = C.getStats().fusion_hit_count;
+    auto rb = C.tryExecuteBackward(nrelub.get(), gy, {x1});
+    CHECK(rb.has_value() && C.getStats().fusion_hit_count == hits);
+    // Without an upstream of its own the Log node cannot close the chain.
+    auto orphan = node("Log", {x2}, nullptr);
+    auto nrelu_o = node("ReLU", {x1}, orphan);
+    C.clearCallScopedState();
+    auto ro = C.tryExecuteBackward(nrelu_o.get(), gy, {x1});
+    CHECK(ro.has_value() && C.getStats().fusion_hit_count == hits);
 }
 
 TEST(config_kill_switches) {

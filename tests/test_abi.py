@@ -107,6 +107,28 @@ def test_elementwise3_and_act_validation():
     assert _rc("c3hip_linear_bwd", 0, 16, 16, None, 16, 16, None, None, 4, 4, 4, 2, None) == native.ERR_INVALID
 
 
+def test_backward_chain_validation():
+    import ctypes
+
+    def arr(t, vals):
+        return (t * max(len(vals), 1))(*vals)
+
+    vp, ci = ctypes.c_void_p, ctypes.c_int
+
+    def rc(dtype, grad, xs, nodes, outs, n):
+        return native.load().c3hip_backward_chain(dtype, grad, arr(vp, xs), arr(ci, nodes), len(nodes),
+                                                  arr(vp, outs), n, None)
+
+    assert rc(native.F32, 16, [16], [native.CHAIN_RELU], [16], -1) == native.ERR_INVALID
+    assert rc(native.BF16, 16, [16], [native.CHAIN_RELU], [16], 4) == native.ERR_UNSUPPORTED
+    assert rc(native.F32, 16, [], [], [], 4) == native.ERR_INVALID                    # no nodes
+    assert rc(native.F32, 16, [16] * 5, [0] * 5, [16] * 5, 4) == native.ERR_INVALID  # beyond the window
+    assert rc(native.F32, 16, [16], [6], [16], 4) == native.ERR_INVALID               # unknown node
+    assert rc(native.F32, 16, [None], [native.CHAIN_TANH], [16], 4) == native.ERR_INVALID
+    assert rc(native.F32, None, [16], [native.CHAIN_RELU], [16], 4) == native.ERR_INVALID
+    assert rc(native.F32, None, [None], [native.CHAIN_RELU], [None], 0) == native.OK  # nothing to do
+
+
 def test_train_step_helper_validation():
     assert _rc("c3hip_softmax_ce", 5, 16, 16, 16, 16, 4, 10, None) == native.ERR_INVALID
     assert _rc("c3hip_softmax_ce", 0, 16, 16, 16, 16, 4, 4096, None) == native.ERR_UNSUPPORTED
