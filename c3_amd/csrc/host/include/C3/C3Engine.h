@@ -59,6 +59,45 @@ struct CompileOptions {
     int opt_level = 3;
     C3Backend backend = C3Backend::HIP;
     bool use_cache = true;
+    // compile() returns a tiered PGOCompiledKernel (include/C3/C3Engine.h:80,
+    // src/C3/C3Engine.cpp:838-861 of the reference).
+    bool pgo_mode = false;
+};
+
+// Execution-time statistics of one kernel (include/C3/C3Engine.h:109-150 of
+// the reference).  Times are host wall times of execute(); for a HIP kernel
+// that is the launch, not the device run.
+struct ProfileData {
+    std::atomic<uint64_t> call_count{0};
+    std::atomic<uint64_t> total_time_ns{0};
+    std::atomic<uint64_t> min_time_ns{UINT64_MAX};
+    std::atomic<uint64_t> max_time_ns{0};
+    std::atomic<uint64_t> last_time_ns{0};
+
+    void record(uint64_t ns) {
+        call_count.fetch_add(1, std::memory_order_relaxed);
+        total_time_ns.fetch_add(ns, std::memory_order_relaxed);
+        last_time_ns.store(ns, std::memory_order_relaxed);
+        uint64_t lo = min_time_ns.load(std::memory_order_relaxed);
+        while (ns < lo && !min_time_ns.compare_exchange_weak(lo, ns, std::memory_order_relaxed)) {}
+        uint64_t hi = max_time_ns.load(std::memory_order_relaxed);
+        while (ns > hi && !max_time_ns.compare_exchange_weak(hi, ns, std::memory_order_relaxed)) {}
+    }
+    uint64_t avgTimeNs() const {
+        const uint64_t n = call_count.load(std::memory_order_relaxed);
+        return n ? total_time_ns.load(std::memory_order_relaxed) / n : 0;
+    }
+};
+
+// How sub-kernel outputs feed the next sub-kernel (include/C3/GraphMerger.h:46-62
+// of the reference): links[i] connects output from_output of sub i to input
+// to_input of sub i + 1 (SIZE_MAX: not connected).
+struct MergeLink {
+    size_t from_output;
+    size_t to_input;
+};
+struct MergeSpec {
+    std::vector<MergeLink> links;  // sub count - 1 entries
 };
 
 // What a compile produces: one kernel family entry of the C ABI.
@@ -88,6 +127,7 @@ struct KernelSpec {
     bool transA = false, transB = false;          // MatMul
     int axis = 0;                                 // SumReduce
     std::vector<int> chain;                       // C3HIP_CHAIN_* per node, BackwardChain
+    std::string tile;                             // forced GEMM tile (c3hip_set_gemm_tile); "" = size heuristic
     std::vector<std::vector<size_t>> input_shapes;
     std::vector<size_t> out_shape;
     DType dtype = DType::kFloat;
@@ -95,6 +135,12 @@ struct KernelSpec {
     std::string toString() const;
     // C ABI module the kernel lives in ("elementwise", "gemm_f32", "gemm_bf16", "reduce").
     std::string moduleName() const;
+    // Shapes and element types of the kernel's outputs, in execute() order.
+    std::vector<std::pair<std::vector<size_t>, DType>> outputDescs() const;
+    // Element type expected of input j.
+    DType inputDtype(size_t j) const;
+    // Whether the kernel runs a GEMM whose tile a tuner may choose.
+    bool hasGemm() const;
 };
 
 struct C3CacheStats {
@@ -114,6 +160,30 @@ public:
     std::shared_ptr<CompiledKernel> compile(const KernelSpec& spec, const CompileOptions& opts = {});
     CompileFuture compileAsync(const KernelSpec& spec, const CompileOptions& opts = {});
 
+    // Several kernels chained by a MergeSpec into one CompiledKernel whose
+    // inputs are the unlinked inputs of every sub-kernel in (sub, input)
+    // order and whose outputs are the last sub-kernel's (src/C3/C3Engine.cpp
+    // compileMerged*, src/C3/GraphMerger.cpp:75-245).  The sub-kernels launch
+    // back to back on the current stream; linked tensors stay on the device.
+    // Throws std::invalid_argument for a spec that does not validate and
+    // std::runtime_error when a sub-kernel does not compile.
+    std::shared_ptr<CompiledKernel> compileMerged(const std::vector<KernelSpec>& subs, const MergeSpec& spec,
+                                                  const CompileOptions& opts = {});
+    std::shared_ptr<CompiledKernel> compileMergedSequential(const std::vector<KernelSpec>& subs,
+                                                            const CompileOptions& opts = {});
+    // Background compileMerged; calls for one (subs, spec, opts) share one future.
+    CompileFuture compileMergedAsync(const std::vector<KernelSpec>& subs, const MergeSpec& spec,
+                                     const CompileOptions& opts = {});
+    // compileMerged behind the PGO tiers (opts.pgo_mode forced on).
+    std::shared_ptr<CompiledKernel> compileMergedPGO(const std::vector<KernelSpec>& subs, const MergeSpec& spec,
+                                                     const CompileOptions& opts = {});
+    std::shared_ptr<CompiledKernel> compileMergedPGOSequential(const std::vector<KernelSpec>& subs,
+                                                               const CompileOptions& opts = {});
+    // Profile data of a pgo_mode cache key (created on first use).
+    std::shared_ptr<ProfileData> profileData(const std::string& key);
+    // A PGO tier's compile failure, also kept as the engine's last error (ADR-010 of the reference).
+    void recordCompileError(const std::string& tier, const std::string& reason);
+
     void setCompileTimeoutMs(uint32_t ms) { compile_timeout_ms_.store(ms); }
     uint32_t getCompileTimeoutMs() const { return compile_timeout_ms_.load(); }
     std::string getLastCompileError() const;
@@ -132,6 +202,8 @@ private:
 
     mutable std::mutex mu_;
     std::unordered_map<std::string, std::shared_ptr<CompiledKernel>> cache_;  // key: opt|spec
+    std::unordered_map<std::string, std::shared_ptr<ProfileData>> profiles_;
+    std::unordered_map<std::string, CompileFuture> merged_async_;
     std::vector<std::future<void>> workers_;
     std::string last_error_;
     Factory factory_;

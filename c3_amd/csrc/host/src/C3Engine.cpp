@@ -5,8 +5,10 @@
 #include <cstdio>
 #include <sstream>
 
+#include "C3/GraphMerger.h"
 #include "C3/HipCompiledKernel.h"
 #include "C3/JITCache.h"
+#include "C3/PGOManager.h"
 #include "C3/RollingHash.h"
 #include "c3hip.h"
 
@@ -77,6 +79,7 @@ std::string KernelSpec::toString() const {
         ss << "|chain=";
         for (int c : chain) ss << c << ",";
     }
+    if (!tile.empty()) ss << "|tile=" << tile;
     ss << "|in=";
     for (const auto& s : input_shapes) ss << shapeToString(s) << ";";
     ss << "|out=" << shapeToString(out_shape);
@@ -93,6 +96,45 @@ std::string KernelSpec::moduleName() const {
         case KernelKind::SumReduce: return "reduce";
         case KernelKind::AddBackwardLhs: return "";
         default: return dtype == DType::kBFloat16 ? "gemm_bf16" : "gemm_f32";
+    }
+}
+
+std::vector<std::pair<std::vector<size_t>, DType>> KernelSpec::outputDescs() const {
+    switch (kind) {
+        case KernelKind::LinearBwd: {
+            // [dY, X, W, Y] -> dX (X's type), dW and db (fp32)
+            if (input_shapes.size() != 4) return {};
+            const auto& X = input_shapes[1];
+            const auto& W = input_shapes[2];
+            if (X.size() != 2 || W.size() != 2) return {};
+            return {{X, dtype}, {{X[1], W[1]}, DType::kFloat}, {{W[1]}, DType::kFloat}};
+        }
+        case KernelKind::BackwardChain: {
+            std::vector<std::pair<std::vector<size_t>, DType>> o;
+            for (size_t k = 0; k < chain.size(); ++k) o.push_back({out_shape, DType::kFloat});
+            return o;
+        }
+        case KernelKind::MatMul:
+        case KernelKind::LinearFwd:
+        case KernelKind::MatMulBackwardA:
+        case KernelKind::MatMulBackwardB: return {{out_shape, dtype}};
+        default: return {{out_shape, DType::kFloat}};
+    }
+}
+
+DType KernelSpec::inputDtype(size_t j) const {
+    if (kind == KernelKind::LinearFwd && j == 2) return DType::kFloat;  // the bias row
+    return dtype;
+}
+
+bool KernelSpec::hasGemm() const {
+    switch (kind) {
+        case KernelKind::MatMul:
+        case KernelKind::LinearFwd:
+        case KernelKind::LinearBwd:
+        case KernelKind::MatMulBackwardA:
+        case KernelKind::MatMulBackwardB: return true;
+        default: return false;
     }
 }
 
@@ -122,8 +164,26 @@ bool C3Engine::hasFactoryForTest() const {
     return static_cast<bool>(factory_);
 }
 
+std::shared_ptr<ProfileData> C3Engine::profileData(const std::string& key) {
+    std::lock_guard<std::mutex> lk(mu_);
+    auto& p = profiles_[key];
+    if (!p) p = std::make_shared<ProfileData>();
+    return p;
+}
+
+void C3Engine::recordCompileError(const std::string& tier, const std::string& reason) {
+    setLastError("[" + tier + "] " + reason);
+}
+
 std::shared_ptr<CompiledKernel> C3Engine::compile(const KernelSpec& spec, const CompileOptions& opts) {
     if (shutting_down_.load()) return nullptr;
+    if (opts.pgo_mode) {
+        // Tiered kernel, one per (options, spec) (src/C3/C3Engine.cpp:838-861).
+        auto& pgo = PGOManager::getInstance();
+        if (!pgo.isEnabled()) pgo.setEnabled(true);
+        const std::string key = "pgo|" + std::to_string(opts.opt_level) + "|" + spec.toString();
+        return pgo.registerKernel(PGOPlan{{spec}, {}}, opts, key, profileData(key), *this);
+    }
     const std::string ckey = std::to_string(opts.opt_level) + "|" + spec.toString();
     Factory factory;
     {
@@ -180,6 +240,73 @@ C3Engine::CompileFuture C3Engine::compileAsync(const KernelSpec& spec, const Com
     return watch;
 }
 
+std::shared_ptr<CompiledKernel> C3Engine::compileMerged(const std::vector<KernelSpec>& subs, const MergeSpec& spec,
+                                                        const CompileOptions& opts) {
+    const std::string err = GraphMerger::validate(subs, spec);
+    if (!err.empty()) throw std::invalid_argument("C3Engine::compileMerged: " + err);
+    const std::string key = std::to_string(opts.opt_level) + "|" + GraphMerger::mergedCacheKey(subs, spec);
+    {
+        std::lock_guard<std::mutex> lk(mu_);
+        auto it = cache_.find(key);
+        if (it != cache_.end()) {
+            hits_++;
+            return it->second;
+        }
+    }
+    CompileOptions sub_opts = opts;
+    sub_opts.pgo_mode = false;
+    std::vector<std::shared_ptr<CompiledKernel>> ks;
+    for (size_t i = 0; i < subs.size(); ++i) {
+        auto k = compile(subs[i], sub_opts);
+        if (!k)
+            throw std::runtime_error("C3Engine::compileMerged: sub-kernel " + std::to_string(i) +
+                                     " did not compile: " + getLastCompileError());
+        ks.push_back(std::move(k));
+    }
+    auto merged = std::make_shared<MergedCompiledKernel>(std::move(ks), subs, spec, key, opts.opt_level);
+    std::lock_guard<std::mutex> lk(mu_);
+    if (cache_.size() >= 256) cache_.erase(cache_.begin());
+    cache_.emplace(key, merged);
+    return merged;
+}
+
+std::shared_ptr<CompiledKernel> C3Engine::compileMergedSequential(const std::vector<KernelSpec>& subs,
+                                                                  const CompileOptions& opts) {
+    return compileMerged(subs, GraphMerger::makeSequentialSpec(subs), opts);
+}
+
+C3Engine::CompileFuture C3Engine::compileMergedAsync(const std::vector<KernelSpec>& subs, const MergeSpec& spec,
+                                                     const CompileOptions& opts) {
+    const std::string key = std::to_string(opts.opt_level) + "|" + std::to_string(opts.pgo_mode) + "|" +
+                            GraphMerger::mergedCacheKey(subs, spec);
+    std::lock_guard<std::mutex> lk(mu_);
+    auto it = merged_async_.find(key);
+    if (it != merged_async_.end()) return it->second;
+    auto fut = std::async(std::launch::async, [this, subs, spec, opts]() -> std::shared_ptr<CompiledKernel> {
+                   return opts.pgo_mode ? compileMergedPGO(subs, spec, opts) : compileMerged(subs, spec, opts);
+               }).share();
+    merged_async_.emplace(key, fut);
+    workers_.push_back(std::async(std::launch::async, [fut] { fut.wait(); }));
+    return fut;
+}
+
+std::shared_ptr<CompiledKernel> C3Engine::compileMergedPGO(const std::vector<KernelSpec>& subs, const MergeSpec& spec,
+                                                           const CompileOptions& opts) {
+    const std::string err = GraphMerger::validate(subs, spec);
+    if (!err.empty()) throw std::invalid_argument("C3Engine::compileMergedPGO: " + err);
+    CompileOptions pgo_opts = opts;
+    pgo_opts.pgo_mode = true;
+    auto& pgo = PGOManager::getInstance();
+    if (!pgo.isEnabled()) pgo.setEnabled(true);
+    const std::string key = "pgo|" + std::to_string(opts.opt_level) + "|" + GraphMerger::mergedCacheKey(subs, spec);
+    return pgo.registerKernel(PGOPlan{subs, spec}, pgo_opts, key, profileData(key), *this);
+}
+
+std::shared_ptr<CompiledKernel> C3Engine::compileMergedPGOSequential(const std::vector<KernelSpec>& subs,
+                                                                     const CompileOptions& opts) {
+    return compileMergedPGO(subs, GraphMerger::makeSequentialSpec(subs), opts);
+}
+
 C3CacheStats C3Engine::getCacheStats() const {
     C3CacheStats s;
     s.hits = hits_.load();
@@ -192,11 +319,18 @@ C3CacheStats C3Engine::getCacheStats() const {
 }
 
 void C3Engine::clearCache() {
-    std::lock_guard<std::mutex> lk(mu_);
-    cache_.clear();
+    {
+        std::lock_guard<std::mutex> lk(mu_);
+        cache_.clear();
+        profiles_.clear();
+        merged_async_.clear();
+    }
+    // The tiered kernels go with the cache (src/C3/C3Engine.cpp:1572-1574).
+    PGOManager::getInstance().clear();
 }
 
 void C3Engine::shutdown() {
+    PGOManager::getInstance().shutdown();  // background compile chains first
     shutting_down_.store(true);
     std::vector<std::future<void>> ws;
     {

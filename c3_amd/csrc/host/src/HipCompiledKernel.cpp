@@ -29,6 +29,18 @@ void requireDevice(const Tensor& t, const char* what) {
     if (t.device() != DeviceType::kHIP) throw std::runtime_error(std::string(what) + ": tensor is not on a HIP device");
 }
 
+// Forces the spec's GEMM tile on this thread for the duration of one launch.
+struct TileGuard {
+    explicit TileGuard(const KernelSpec& s) : dt(hipDtype(s.dtype)), on(!s.tile.empty()) {
+        if (on) check(c3hip_set_gemm_tile(dt, s.tile.c_str()), "c3hip_set_gemm_tile");
+    }
+    ~TileGuard() {
+        if (on) (void)c3hip_set_gemm_tile(dt, nullptr);
+    }
+    int dt;
+    bool on;
+};
+
 }  // namespace
 
 void setCurrentStream(void* stream) { t_stream = stream; }
@@ -60,6 +72,7 @@ std::vector<Tensor> HipCompiledKernel::execute(const std::vector<Tensor>& in) {
         }
     };
     void* st = t_stream;
+    TileGuard tile_guard(s);
     switch (s.kind) {
         case KernelKind::Elementwise: {
             const bool binary = s.ew_op == C3HIP_EW_ADD || s.ew_op == C3HIP_EW_SUB || s.ew_op == C3HIP_EW_MUL ||

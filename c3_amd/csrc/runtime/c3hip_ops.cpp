@@ -77,14 +77,18 @@ const Tile* find_tile(const Tile* tiles, size_t n, const char* name) {
     return nullptr;
 }
 
-// fp32 tile per GEMM kind and size (C3_HIP_GEMM_TILE overrides, for sweeps).  Measured on MI355X at 8192x4096x4096:
+// Tile forced for the calling thread (c3hip_set_gemm_tile); empty = none.
+thread_local std::string t_tile_f32, t_tile_bf16;
+
+// fp32 tile per GEMM kind and size (c3hip_set_gemm_tile, then C3_HIP_GEMM_TILE, override it).  Measured on MI355X at 8192x4096x4096:
 // the weight-gradient kinds (A read k-major, k = M = 8192 deep) run at
 // 121 TFLOP/s on 256x128 tiles against 112 on 128x128; forward and dX are
 // best on 128x128.  Small grids use 64x64 so every CU gets a block.
 const Tile* choose_f32_tile(Kind kind, int64_t M, int64_t N) {
     const size_t nt = sizeof(kF32Tiles) / sizeof(kF32Tiles[0]);
-    if (const char* env = std::getenv("C3_HIP_GEMM_TILE")) {
-        if (const Tile* t = find_tile(kF32Tiles, nt, env)) return t;
+    const char* forced = !t_tile_f32.empty() ? t_tile_f32.c_str() : std::getenv("C3_HIP_GEMM_TILE");
+    if (forced) {
+        if (const Tile* t = find_tile(kF32Tiles, nt, forced)) return t;
     }
     const bool dw = kind == Kind::Dw || kind == Kind::DwMask;
     const int64_t blocks256 = ((M + 255) / 256) * ((N + 127) / 128);
@@ -94,10 +98,14 @@ const Tile* choose_f32_tile(Kind kind, int64_t M, int64_t N) {
     return &kF32Tiles[0];
 }
 
+const char* bf16_forced() {
+    return !t_tile_bf16.empty() ? t_tile_bf16.c_str() : std::getenv("C3_HIP_GEMM_TILE_BF16");
+}
+
 const Tile* choose_bf16_tile(int64_t M, int64_t N) {
     const size_t nt = sizeof(kBf16Tiles) / sizeof(kBf16Tiles[0]);
-    if (const char* env = std::getenv("C3_HIP_GEMM_TILE_BF16")) {
-        if (const Tile* t = find_tile(kBf16Tiles, nt, env)) return t;
+    if (const char* forced = bf16_forced()) {
+        if (const Tile* t = find_tile(kBf16Tiles, nt, forced)) return t;
     }
     const int64_t blocks128 = ((M + 127) / 128) * ((N + 127) / 128);
     if (blocks128 >= 256) return &kBf16Tiles[1];
@@ -110,16 +118,25 @@ const Tile* choose_bf16_tile(int64_t M, int64_t N) {
 // the chip.
 const Tile kBf16Direct[] = {{"d256w8", 256, 256, 512, 64}, {"d256rq", 256, 256, 256, 64}};
 
-const Tile* choose_bf16_direct(Kind kind, const GemmArgs& a) {
+bool direct_eligible(Kind kind, const GemmArgs& a, const Tile* t) {
+    if (kind == Kind::DxMask || kind == Kind::DwMask || a.db != nullptr) return false;
+    return a.K > 0 && a.M >= 8 && a.N >= 8 && a.K % t->bk == 0;
+}
+
+// Sets *unsupported when the calling thread forced a direct tile this
+// problem cannot use.
+const Tile* choose_bf16_direct(Kind kind, const GemmArgs& a, bool* unsupported) {
+    *unsupported = false;
+    if (const char* forced = bf16_forced()) {
+        const Tile* t = find_tile(kBf16Direct, sizeof(kBf16Direct) / sizeof(kBf16Direct[0]), forced);
+        if (!t) return nullptr;  // a register-staged tile was asked for
+        if (direct_eligible(kind, a, t)) return t;
+        *unsupported = !t_tile_bf16.empty();
+        return nullptr;
+    }
     if (kind == Kind::DxMask || kind == Kind::DwMask || a.db != nullptr) return nullptr;
     if (a.K == 0) return nullptr;
     if (a.M < 8 || a.N < 8) return nullptr;
-    const char* env = std::getenv("C3_HIP_GEMM_TILE_BF16");
-    if (env) {
-        if (const Tile* t = find_tile(kBf16Direct, sizeof(kBf16Direct) / sizeof(kBf16Direct[0]), env))
-            return a.K % t->bk == 0 ? t : nullptr;
-        return nullptr;  // an explicit non-direct tile was asked for
-    }
     const int64_t blocks = ((a.M + 255) / 256) * ((a.N + 255) / 256);
     if (blocks < 64) return nullptr;
     const Tile* t = &kBf16Direct[0];
@@ -148,7 +165,13 @@ int run_gemm(int dtype, Kind kind, const GemmArgs& a0, bool a_kc, bool b_kc, hip
         if (!bf16_vec_ok(a_kc, a.M, a.K, a.lda, a.A, a.Amask) || !bf16_vec_ok(b_kc, a.N, a.K, a.ldb, a.B, a.Bmask))
             return set_error(C3HIP_ERR_UNSUPPORTED,
                              "bf16 GEMM needs 16-byte aligned operands and contiguous extents that are multiples of 8");
-        if (const Tile* d = choose_bf16_direct(kind, a)) {
+        bool unsupported = false;
+        const Tile* d = choose_bf16_direct(kind, a, &unsupported);
+        if (unsupported)
+            return set_error(C3HIP_ERR_UNSUPPORTED, std::string("tile ") + t_tile_bf16 +
+                                                        " cannot run this GEMM (masked operand, db side output, "
+                                                        "K not a multiple of its k depth, or M or N below 8)");
+        if (d) {
             char name[96];
             std::snprintf(name, sizeof(name), "c3_gemm_bf16_%s_%s", kind_name(kind), d->name);
             const int64_t blocks = ((a.M + 255) / 256) * ((a.N + 255) / 256);
@@ -345,6 +368,44 @@ int c3hip_elementwise3(int op, int dtype, const void* a, const void* b, const vo
     const int64_t blocks = std::min<int64_t>((n + 255) / 256, 1 << 16);
     void* args[] = {(void*)&a, (void*)&b, (void*)&c, &out, &n};
     return launch("c3_ew3_div_bwd_b_f32", dim3((unsigned)blocks), dim3(256), args, (hipStream_t)stream);
+}
+
+int c3hip_set_gemm_tile(int dtype, const char* name) {
+    clear_error();
+    int rc = check_dtype(dtype);
+    if (rc) return rc;
+    std::string& slot = dtype == C3HIP_BF16 ? t_tile_bf16 : t_tile_f32;
+    if (!name || !*name) {
+        slot.clear();
+        return C3HIP_OK;
+    }
+    const bool known =
+        dtype == C3HIP_BF16
+            ? (find_tile(kBf16Tiles, sizeof(kBf16Tiles) / sizeof(kBf16Tiles[0]), name) ||
+               find_tile(kBf16Direct, sizeof(kBf16Direct) / sizeof(kBf16Direct[0]), name))
+            : find_tile(kF32Tiles, sizeof(kF32Tiles) / sizeof(kF32Tiles[0]), name) != nullptr;
+    if (!known) return set_error(C3HIP_ERR_INVALID, std::string("unknown GEMM tile ") + name);
+    slot = name;
+    return C3HIP_OK;
+}
+
+int c3hip_gemm_tile_names(int dtype, char* buf, size_t buflen) {
+    clear_error();
+    int rc = check_dtype(dtype);
+    if (rc) return rc;
+    std::string names;
+    auto add = [&](const Tile* tiles, size_t n) {
+        for (size_t i = 0; i < n; ++i) names += (names.empty() ? "" : ",") + std::string(tiles[i].name);
+    };
+    if (dtype == C3HIP_BF16) {
+        add(kBf16Tiles, sizeof(kBf16Tiles) / sizeof(kBf16Tiles[0]));
+        add(kBf16Direct, sizeof(kBf16Direct) / sizeof(kBf16Direct[0]));
+    } else {
+        add(kF32Tiles, sizeof(kF32Tiles) / sizeof(kF32Tiles[0]));
+    }
+    if (!buf || buflen < names.size() + 1) return set_error(C3HIP_ERR_INVALID, "buffer too small");
+    std::memcpy(buf, names.c_str(), names.size() + 1);
+    return C3HIP_OK;
 }
 
 int c3hip_backward_chain(int dtype, const void* grad, const void* const* x, const int* nodes, int num_nodes,

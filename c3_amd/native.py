@@ -46,6 +46,8 @@ SIGNATURES = {
     "c3hip_code_object_path": (_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_size_t]),
     "c3hip_elementwise": (_int, [_int, _int, _vp, _vp, _f, _vp, _i64, _i64, _vp]),
     "c3hip_elementwise3": (_int, [_int, _int, _vp, _vp, _vp, _vp, _i64, _vp]),
+    "c3hip_set_gemm_tile": (_int, [_int, ctypes.c_char_p]),
+    "c3hip_gemm_tile_names": (_int, [_int, ctypes.c_char_p, ctypes.c_size_t]),
     "c3hip_backward_chain": (_int, [_int, _vp, ctypes.POINTER(_vp), ctypes.POINTER(_int), _int,
                                     ctypes.POINTER(_vp), _i64, _vp]),
     "c3hip_matmul": (_int, [_int, _vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _vp]),
@@ -116,6 +118,17 @@ def elementwise(op: int, dtype: int, a: int, b: int | None, alpha: float, out: i
 
 def elementwise3(op: int, dtype: int, a: int, b: int, c: int, out: int, n: int, stream: int = 0) -> None:
     _check("c3hip_elementwise3", load().c3hip_elementwise3(op, dtype, a, b, c, out, n, stream))
+
+
+def set_gemm_tile(dtype: int, name: str | None) -> None:
+    """Force the calling thread's GEMM tile for dtype (None: size heuristic)."""
+    _check("c3hip_set_gemm_tile", load().c3hip_set_gemm_tile(dtype, name.encode() if name else None))
+
+
+def gemm_tile_names(dtype: int) -> list[str]:
+    buf = ctypes.create_string_buffer(512)
+    _check("c3hip_gemm_tile_names", load().c3hip_gemm_tile_names(dtype, buf, len(buf)))
+    return buf.value.decode().split(",")
 
 
 def backward_chain(dtype: int, grad: int, xs, nodes, outs, n: int, stream: int = 0) -> None:

@@ -143,6 +143,22 @@ int c3hip_elementwise3(int op, int dtype, const void* a, const void* b, const vo
                        void* stream);
 
 /*
+ * Force the GEMM tile of dtype's GEMMs launched by the calling thread (every
+ * c3hip_matmul / c3hip_linear_fwd / c3hip_linear_bwd call that follows), by
+ * one of the names c3hip_gemm_tile_names lists; NULL or "" restores the size
+ * heuristic.  A forced direct-to-LDS bf16 tile (d256*) that cannot run a
+ * problem makes that call fail with C3HIP_ERR_UNSUPPORTED (no silent
+ * fallback).  Replaces the optimisation-level choice of the reference's PGO
+ * tiers (PGOCompiledKernel::compileO2 / compileOfast,
+ * src/C3/PGOManager.cpp:292-366): here a tier differs by launch configuration,
+ * which the tuner picks by timing the candidates on the caller's stream.
+ */
+int c3hip_set_gemm_tile(int dtype, const char* name);
+
+/* Comma-separated GEMM tile names of dtype into buf (NUL-terminated). */
+int c3hip_gemm_tile_names(int dtype, char* buf, size_t buflen);
+
+/*
  * Fused backward of a chain of num_nodes (1..C3HIP_CHAIN_MAX_NODES)
  * single-input elementwise nodes over n contiguous elements, node 0 the most
  * downstream: g_0 = grad, g_{k+1} = rule(nodes[k], g_k, x[k]) and

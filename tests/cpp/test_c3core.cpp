@@ -21,6 +21,8 @@
 #include "C3/C3HotPathManager.h"
 #include "C3/C3KernelRegistry.h"
 #include "C3/FusionCostModel.h"
+#include "C3/GraphMerger.h"
+#include "C3/PGOManager.h"
 #include "C3/JITCache.h"
 #include "C3/RegionFusion.h"
 #include "C3/RollingHash.h"
@@ -691,6 +693,218 @@ TEST(backward_capture_rules_and_keys) {
     CHECK(!B.tryExecuteBackward("Softmax", g, {x}).has_value());
     const auto st = B.getStats();
     CHECK(st.cache_hit_count == 3 && st.cache_miss_count == 3 && st.compiles_submitted == 5);
+}
+
+// ---------------------------------------------------- merged kernels, PGO --
+namespace {
+KernelSpec linearSpec(size_t M, size_t K, size_t N, int act) {
+    KernelSpec s;
+    s.kind = KernelKind::LinearFwd;
+    s.op_seq = {op::MatMul, op::Add};
+    if (act == 1) s.op_seq.push_back(op::ReLU);
+    s.act = act;
+    s.input_shapes = {{M, K}, {K, N}, {N}};
+    s.out_shape = {M, N};
+    return s;
+}
+
+// relu(X W + b) on the host, in the kernel's order.
+std::vector<float> hostLinear(const std::vector<float>& X, const std::vector<float>& W, const std::vector<float>& b,
+                              size_t M, size_t K, size_t N, bool relu) {
+    std::vector<float> Y(M * N);
+    for (size_t i = 0; i < M; ++i)
+        for (size_t j = 0; j < N; ++j) {
+            float acc = 0;
+            for (size_t k = 0; k < K; ++k) acc += X[i * K + k] * W[k * N + j];
+            acc += b[j];
+            Y[i * N + j] = relu ? (acc > 0 ? acc : 0.f) : acc;
+        }
+    return Y;
+}
+
+// PGO test rig: host kernels, synchronous compile chains, a counting interpreter.
+struct PgoRig {
+    HostBackend hb;
+    std::atomic<int> interpreted{0};
+    PgoRig() {
+        auto& P = PGOManager::getInstance();
+        P.config() = PGOConfig{};
+        P.config().async_compilation = false;
+        P.setInterpreterForTest([this](const KernelSpec& s, const std::vector<Tensor>& in) {
+            interpreted++;
+            return HostKernel(s, 0).execute(in);
+        });
+    }
+    ~PgoRig() {
+        PGOManager::getInstance().setInterpreterForTest(nullptr);
+        PGOManager::getInstance().config() = PGOConfig{};
+        PGOManager::getInstance().clear();
+    }
+};
+}  // namespace
+
+TEST(graph_merger_validate_and_wiring) {
+    const auto a = linearSpec(8, 12, 6, 1), b = linearSpec(8, 6, 4, 1), c = linearSpec(8, 4, 3, 0);
+    CHECK_EQ(GraphMerger::validate({a, b, c}, GraphMerger::makeSequentialSpec({a, b, c})), std::string());
+    CHECK(GraphMerger::validate({}, {}).find("no sub-kernels") != std::string::npos);
+    CHECK(GraphMerger::validate({a, b}, {}).find("links count") != std::string::npos);
+    CHECK(GraphMerger::validate({a, b}, MergeSpec{{{1, 0}}}).find("from_output") != std::string::npos);
+    CHECK(GraphMerger::validate({a, b}, MergeSpec{{{0, 3}}}).find("to_input") != std::string::npos);
+    CHECK(GraphMerger::validate({a, c}, MergeSpec{{{0, 0}}}).find("desc mismatch") != std::string::npos);
+    CHECK(GraphMerger::validate({a, b}, MergeSpec{{{0, 1}}}).find("desc mismatch") != std::string::npos);
+    auto info = GraphMerger::merge({a, b, c}, GraphMerger::makeSequentialSpec({a, b, c}));
+    const std::vector<std::pair<size_t, size_t>> ext = {{0, 0}, {0, 1}, {0, 2}, {1, 1}, {1, 2}, {2, 1}, {2, 2}};
+    CHECK(info.external_inputs == ext);
+    CHECK(info.input_source[1][0] == 0 && info.input_source[1][1] == SIZE_MAX);
+    // An unconnected link leaves the next sub's input external.
+    auto open = GraphMerger::merge({a, a}, MergeSpec{{{0, SIZE_MAX}}});
+    CHECK_EQ(open.external_inputs.size(), size_t(6));
+    const std::string key = GraphMerger::mergedCacheKey({a, b}, GraphMerger::makeSequentialSpec({a, b}));
+    CHECK(key.rfind("merged_v4_2|G0{", 0) == 0 && key.find("|L0>0|G1{") != std::string::npos);
+    CHECK(key != GraphMerger::mergedCacheKey({a, b}, MergeSpec{{{0, SIZE_MAX}}}));
+    bool threw = false;
+    try {
+        GraphMerger::merge({a, c}, MergeSpec{{{0, 0}}});
+    } catch (const std::invalid_argument&) {
+        threw = true;
+    }
+    CHECK(threw);
+}
+
+TEST(merged_kernel_runs_layers_in_order) {
+    HostBackend hb;
+    auto& E = C3Engine::getInstance();
+    const size_t M = 2, K = 3, H = 2, N = 2;
+    const std::vector<float> X = {1, -2, 3, 0, 1, -1}, W1 = {1, 0, -1, 2, 1, 1}, b1 = {0.5f, -1},
+                             W2 = {1, -1, 2, 1}, b2 = {0, 1};
+    const auto s1 = linearSpec(M, K, H, 1), s2 = linearSpec(M, H, N, 0);
+    auto k = E.compileMergedSequential({s1, s2});
+    CHECK(k && k == E.compileMergedSequential({s1, s2}));  // cached
+    auto out = k->execute({host({M, K}, X), host({K, H}, W1), host({H}, b1), host({H, N}, W2), host({N}, b2)});
+    CHECK_EQ(out.size(), size_t(1));
+    CHECK(vals(out[0]) == hostLinear(hostLinear(X, W1, b1, M, K, H, true), W2, b2, M, H, N, false));
+    auto f = E.compileMergedAsync({s1, s2}, GraphMerger::makeSequentialSpec({s1, s2}));
+    CHECK(f.get() != nullptr && f.get().get() == E.compileMergedAsync({s1, s2}, GraphMerger::makeSequentialSpec({s1, s2})).get().get());
+    bool threw = false;
+    try {
+        E.compileMerged({s1, s1}, GraphMerger::makeSequentialSpec({s1, s1}));
+    } catch (const std::invalid_argument&) {
+        threw = true;
+    }
+    CHECK(threw);
+    // Wrong input count.
+    threw = false;
+    try {
+        k->execute({host({M, K}, X)});
+    } catch (const std::runtime_error&) {
+        threw = true;
+    }
+    CHECK(threw);
+}
+
+// A PGO kernel: eager first (the interpreter) and the compile chain; then
+// the Ofast tuner times the three fp32 tiles on real calls (the host kernels
+// sleep per tile, t128x128 fastest) and keeps the fastest; results are the
+// same on every tier.
+TEST(pgo_tiers_tune_and_deopt) {
+    PgoRig rig;
+    auto& E = C3Engine::getInstance();
+    auto& P = PGOManager::getInstance();
+    E.setFactoryForTest([](const KernelSpec& sp, const CompileOptions& o) -> std::shared_ptr<CompiledKernel> {
+        g_built++;
+        auto inner = std::make_shared<HostKernel>(sp, o.opt_level);
+        const int ms = sp.tile == "t64x64" ? 4 : sp.tile == "t256x128" ? 8 : 0;
+        return std::make_shared<ScriptedKernel>(o.opt_level, [inner, ms](const std::vector<Tensor>& in) {
+            if (ms) std::this_thread::sleep_for(std::chrono::milliseconds(ms));
+            return inner->execute(in);
+        });
+    });
+    const size_t M = 3, K = 4, N = 2;
+    const std::vector<float> X = {1, 2, 0, -1, 3, -2, 1, 1, 0, 0, 2, -3}, W = {1, -1, 0, 2, 1, 1, -2, 0}, b = {0.25f, -0.5f};
+    const auto want = hostLinear(X, W, b, M, K, N, true);
+    const std::vector<Tensor> in = {host({M, K}, X), host({K, N}, W), host({N}, b)};
+    CompileOptions po;
+    po.pgo_mode = true;
+    auto k = std::dynamic_pointer_cast<PGOCompiledKernel>(E.compile(linearSpec(M, K, N, 1), po));
+    CHECK(k && k == std::dynamic_pointer_cast<PGOCompiledKernel>(E.compile(linearSpec(M, K, N, 1), po)));
+    CHECK(P.isEnabled() && !k->isPromoted());
+    CHECK(vals(k->execute(in)[0]) == want);  // eager, and the chain compiles (synchronously here)
+    CHECK_EQ(rig.interpreted.load(), 1);
+    CHECK(k->isPromoted() && k->o2Kernel() && k->ofastKernel());
+    auto tuners = k->tuners();
+    CHECK(tuners.size() == 1 && tuners[0] && tuners[0]->candidateCount() == 3);
+    int calls = 1;
+    while (!tuners[0]->tuned() && calls < 40) {
+        CHECK(vals(k->execute(in)[0]) == want);
+        ++calls;
+    }
+    CHECK(tuners[0]->tuned());
+    CHECK_EQ(calls, 1 + 3 * (1 + P.config().tune_samples));
+    CHECK_EQ(tuners[0]->chosen(), std::string("t128x128"));
+    CHECK(vals(k->execute(in)[0]) == want);
+    CHECK_EQ(rig.interpreted.load(), 1);
+    CHECK_EQ(k->profileData().call_count.load(), (uint64_t)calls + 1);
+    // Heat score closed form.
+    const double n = (double)k->profileData().call_count.load(), t = (double)k->profileData().total_time_ns.load();
+    const double want_heat = 0.4 * std::min(1.0, std::log2(1.0 + n) / std::log2(1001.0)) + 0.6 * std::min(1.0, t / 1e9);
+    CHECK(std::fabs(k->computeHeatScore() - want_heat) < 1e-12);
+    auto st = P.getStats();
+    CHECK(st.total_registered == 1 && st.o2_ready == 1 && st.ofast_ready == 1 && st.pending == 0);
+
+    // Deopt: every Ofast candidate throws -> Ofast disabled, O2 serves.
+    E.setFactoryForTest([](const KernelSpec& sp, const CompileOptions& o) -> std::shared_ptr<CompiledKernel> {
+        auto inner = std::make_shared<HostKernel>(sp, o.opt_level);
+        const bool bad = !sp.tile.empty();
+        return std::make_shared<ScriptedKernel>(o.opt_level, [inner, bad](const std::vector<Tensor>& x) {
+            if (bad) throw std::runtime_error("tile cannot run");
+            return inner->execute(x);
+        });
+    });
+    auto k2 = std::dynamic_pointer_cast<PGOCompiledKernel>(E.compile(linearSpec(M, K, N, 0), po));
+    const auto want2 = hostLinear(X, W, b, M, K, N, false);
+    CHECK(vals(k2->execute(in)[0]) == want2);  // eager + chain
+    CHECK(vals(k2->execute(in)[0]) == want2);  // Ofast fails over every candidate -> O2
+    CHECK(k2->isOfastDisabled() && !k2->isO2Disabled() && k2->deoptCount() == 1);
+    CHECK(k2->lastDeoptReason().rfind("ofast:", 0) == 0);
+    CHECK(vals(k2->execute(in)[0]) == want2);
+    CHECK_EQ(k2->deoptCount(), uint64_t(1));
+}
+
+TEST(pgo_backpressure_queue_and_merged_plan) {
+    PgoRig rig;
+    auto& E = C3Engine::getInstance();
+    auto& P = PGOManager::getInstance();
+    P.config().max_concurrent_compilations = 0;  // every chain waits in the queue
+    CompileOptions po;
+    po.pgo_mode = true;
+    const size_t M = 2, K = 3, H = 2, N = 2;
+    const std::vector<float> X = {1, -2, 3, 0, 1, -1}, W1 = {1, 0, -1, 2, 1, 1}, b1 = {0.5f, -1},
+                             W2 = {1, -1, 2, 1}, b2 = {0, 1};
+    const std::vector<Tensor> in = {host({M, K}, X), host({K, H}, W1), host({H}, b1), host({H, N}, W2), host({N}, b2)};
+    const auto want = hostLinear(hostLinear(X, W1, b1, M, K, H, true), W2, b2, M, H, N, false);
+    auto k = std::dynamic_pointer_cast<PGOCompiledKernel>(
+        E.compileMergedPGOSequential({linearSpec(M, K, H, 1), linearSpec(M, H, N, 0)}));
+    CHECK(k != nullptr);
+    CHECK(vals(k->execute(in)[0]) == want);  // eager over both layers
+    CHECK_EQ(rig.interpreted.load(), 2);
+    auto st = P.getStats();
+    CHECK(st.queued == 1 && st.queue_rejections == 1 && st.pending == 1 && !k->isPromoted());
+    P.config().max_concurrent_compilations = 4;
+    P.processQueue();  // runs the queued chain
+    CHECK(k->isPromoted() && P.getStats().queued == 0);
+    CHECK(vals(k->execute(in)[0]) == want);  // Ofast merged: both layers' tuners
+    auto tuners = k->tuners();
+    CHECK(tuners.size() == 2 && tuners[0] && tuners[1]);
+    for (int i = 0; i < 20; ++i) CHECK(vals(k->execute(in)[0]) == want);
+    CHECK(tuners[0]->tuned() && tuners[1]->tuned());
+    CHECK_EQ(rig.interpreted.load(), 2);
+    // promoteAll on a fresh kernel compiles it in the calling thread.
+    auto k3 = std::dynamic_pointer_cast<PGOCompiledKernel>(E.compile(linearSpec(M, K, H, 1), po));
+    CHECK(!k3->isPromoted());
+    P.promoteAll();
+    CHECK(k3->isPromoted());
+    CHECK(vals(k3->execute({in[0], in[1], in[2]})[0]) == hostLinear(X, W1, b1, M, K, H, true));
+    CHECK_EQ(rig.interpreted.load(), 2);
 }
 
 // ------------------------------------------------- fused backward chains --

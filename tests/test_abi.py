@@ -129,6 +129,22 @@ def test_backward_chain_validation():
     assert rc(native.F32, None, [None], [native.CHAIN_RELU], [None], 0) == native.OK  # nothing to do
 
 
+def test_gemm_tile_override_validation():
+    assert native.gemm_tile_names(native.F32) == ["t64x64", "t128x128", "t256x128"]
+    assert native.gemm_tile_names(native.BF16) == ["t64x64", "t128x128", "t256x128", "t256x256", "d256w8", "d256rq"]
+    L = native.load()
+    assert L.c3hip_set_gemm_tile(native.F32, b"d256w8") == native.ERR_INVALID  # a bf16-only tile
+    assert L.c3hip_set_gemm_tile(native.BF16, b"t32x32") == native.ERR_INVALID
+    assert L.c3hip_set_gemm_tile(7, b"t64x64") == native.ERR_INVALID
+    assert L.c3hip_set_gemm_tile(native.F32, b"t128x128") == native.OK
+    assert L.c3hip_set_gemm_tile(native.F32, None) == native.OK
+    assert L.c3hip_set_gemm_tile(native.BF16, b"") == native.OK
+    import ctypes
+
+    small = ctypes.create_string_buffer(8)
+    assert L.c3hip_gemm_tile_names(native.BF16, small, len(small)) == native.ERR_INVALID
+
+
 def test_train_step_helper_validation():
     assert _rc("c3hip_softmax_ce", 5, 16, 16, 16, 16, 4, 10, None) == native.ERR_INVALID
     assert _rc("c3hip_softmax_ce", 0, 16, 16, 16, 16, 4, 4096, None) == native.ERR_UNSUPPORTED

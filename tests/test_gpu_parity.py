@@ -361,3 +361,38 @@ def test_bf16_rejects_unaligned_extents(gpu, stream):
     with pytest.raises(N.C3HipError) as ei:
         N.linear_fwd(N.BF16, ptr(X), ptr(W), None, ptr(Y), 16, 12, 16, 1, stream)
     assert ei.value.code == N.ERR_UNSUPPORTED
+
+
+def test_forced_tile_override(gpu, stream):
+    # The calling thread's tile override (c3hip_set_gemm_tile): results are
+    # the oracle's bit for bit under every tile; a direct tile on a problem it
+    # cannot run is refused, not silently replaced; clearing restores the
+    # heuristic.
+    from tests.parity import dev_bf16
+
+    M, K, Nn = 300, 264, 200
+    X, W, b = ints(95, (M, K)), ints(96, (K, Nn)), ints(97, Nn)
+    rY = O.linear_fwd(X, W, b, 1)
+    try:
+        for tile in N.gemm_tile_names(N.F32):
+            N.set_gemm_tile(N.F32, tile)
+            Y = empty((M, Nn))
+            N.linear_fwd(N.F32, ptr(dev(X)), ptr(dev(W)), ptr(dev(b)), ptr(Y), M, K, Nn, 1, stream)
+            same_bits(host(Y), rY)
+        for tile in N.gemm_tile_names(N.BF16):
+            N.set_gemm_tile(N.BF16, tile)
+            Y = empty((M, Nn), dtype=torch.bfloat16)
+            args = (N.BF16, ptr(dev_bf16(X)), ptr(dev_bf16(W)), ptr(dev(b)), ptr(Y), M, K, Nn, 1, stream)
+            if tile.startswith("d256"):  # K = 264 is not a multiple of the 64-deep k tile
+                with pytest.raises(N.C3HipError) as e:
+                    N.linear_fwd(*args)
+                assert e.value.code == N.ERR_UNSUPPORTED
+                continue
+            N.linear_fwd(*args)
+            same_bits(host(Y), _bf16_round(rY))
+    finally:
+        N.set_gemm_tile(N.F32, None)
+        N.set_gemm_tile(N.BF16, None)
+    Y = empty((M, Nn), dtype=torch.bfloat16)
+    N.linear_fwd(N.BF16, ptr(dev_bf16(X)), ptr(dev_bf16(W)), ptr(dev(b)), ptr(Y), M, K, Nn, 1, stream)
+    same_bits(host(Y), _bf16_round(rY))
