@@ -650,7 +650,156 @@ __device__ __forceinline__ void gemm_bf16_rq_body(const GemmArgs& p) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Ping-pong schedule (suffix _pp): 8 waves, two per SIMD (waves w and w + 4
+// share SIMD w % 4), each computing a 128x64 part of the 256x256 tile
+// (group g = w / 4 takes rows 128g .. 128g + 127, wave w % 4 the columns
+// 64(w % 4) ..).  The two groups alternate between a load phase (fragment
+// reads of one BK-deep k tile from LDS into registers, plus the group's
+// share of the DMA of a later tile) and a compute phase (the MFMAs of the
+// fragments loaded in the previous phase), offset by one phase: while the
+// waves of one group issue MFMAs the other group's waves on the same SIMDs
+// issue LDS traffic, so the matrix core of each SIMD is fed by alternate
+// waves and the LDS reads never stand in its issue queue.  Phases end at
+// block barriers; group 1 passes one extra barrier at the start and skips
+// its last one, so both groups pass the same number.
+// Global phase 2j: group 0 loads tile j, group 1 computes tile j - 1;
+// phase 2j + 1: group 0 computes tile j, group 1 loads tile j.  Tile t sits
+// in stage t % STAGES; its last reader is group 1 in phase 2t + 1, so in
+// phase 2j (group 0) and 2j + 1 (group 1) each group issues its share of
+// tile j + STAGES - 1 into the stage tile j - 1 held.  Tile j + 1 is first
+// read in phase 2j + 2: every wave waits for its own DMA of that tile
+// before the barrier that ends phase 2j + 1.
+// ---------------------------------------------------------------------------
+template <bool AK, bool BKC, int EPI, int BK, int STAGES>
+__device__ __forceinline__ void gemm_bf16_pp_body(const GemmArgs& p) {
+    constexpr int BM = 256, BN = 256, NW = 8, TM = 128, TN = 64, FM = TM / 32, FN = TN / 32;
+    constexpr int KSTEPS = BK / 16;
+    using TA = DirectTile<BM, AK, NW, BK>;
+    using TB = DirectTile<BN, BKC, NW, BK>;
+    constexpr int A_EL = TA::BYTES / 2, B_EL = TB::BYTES / 2, STAGE = A_EL + B_EL;
+    constexpr int NIW = TA::NI + TB::NI;
+    static_assert(STAGES >= 2 && STAGES <= 4, "2 to 4 stages");
+    static_assert((STAGES - 1) * NIW < 64, "outstanding DMA instructions exceed vmcnt");
+
+    __shared__ __attribute__((aligned(1024))) unsigned short smem[STAGES * STAGE];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int grp = wave >> 2;
+    const int r0 = grp * TM, c0 = (wave & 3) * TN;
+
+    int tm, tn;
+    tile_coords<8>(p.M, p.N, BM, BN, tm, tn);
+    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+
+    const unsigned short* A = (const unsigned short*)p.A;
+    const unsigned short* B = (const unsigned short*)p.B;
+    TA la;
+    TB lb;
+    la.init(wave, lane, p.lda, m0, p.M);
+    lb.init(wave, lane, p.ldb, n0, p.N);
+    const int64_t a_kstep = AK ? BK : (int64_t)BK * p.lda;
+    const int64_t b_kstep = BKC ? BK : (int64_t)BK * p.ldb;
+
+    f32x16 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+    const int nk = (int)(p.K / BK);
+#pragma unroll
+    for (int u = 0; u < STAGES; ++u) {
+        if (u < nk) {
+            la.issue(A + (int64_t)u * a_kstep, smem + u * STAGE, wave);
+            lb.issue(B + (int64_t)u * b_kstep, smem + u * STAGE + A_EL, wave);
+        }
+    }
+    // Tile 0 landed everywhere (up to STAGES - 1 later tiles may be in flight).
+    wait_tiles_after<NIW, STAGES>(min(nk - 1, STAGES - 1));
+    __syncthreads();
+    if (grp == 1) __syncthreads();
+
+    bf16x8 fa[KSTEPS][FM], fb[KSTEPS][FN];
+    for (int j = 0; j < nk; ++j) {
+        // Load phase of tile j.
+        const unsigned short* As = smem + (j % STAGES) * STAGE;
+        if (j >= 1 && j + STAGES - 1 < nk) {
+            unsigned short* Sd = smem + ((j + STAGES - 1) % STAGES) * STAGE;
+            la.issue(A + (int64_t)(j + STAGES - 1) * a_kstep, Sd, wave);
+            lb.issue(B + (int64_t)(j + STAGES - 1) * b_kstep, Sd + A_EL, wave);
+        }
+#pragma unroll
+        for (int s = 0; s < KSTEPS; ++s) {
+#pragma unroll
+            for (int i = 0; i < FM; ++i) fa[s][i] = TA::frag(As, r0 + 32 * i, s, lane);
+#pragma unroll
+            for (int q = 0; q < FN; ++q) fb[s][q] = TB::frag(As + A_EL, c0 + 32 * q, s, lane);
+        }
+        // Tiles issued so far: up to min(j + STAGES - 1, nk - 1); tile j + 1 must land.
+        const int after = min(STAGES - 2, nk - 2 - j);
+        if (grp == 1) wait_tiles_after<NIW, STAGES - 1>(max(after, 0));
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+        // Compute phase of tile j.
+#pragma unroll
+        for (int s = 0; s < KSTEPS; ++s)
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int q = 0; q < FN; ++q)
+                    acc[i][q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[s][i], fb[s][q], acc[i][q], 0, 0, 0);
+        if (grp == 0) wait_tiles_after<NIW, STAGES - 1>(max(after, 0));
+        __builtin_amdgcn_sched_barrier(0);
+        if (grp == 0 || j + 1 < nk) __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    const int r = lane & 31, g = lane >> 5;
+#pragma unroll
+    for (int q = 0; q < FN; ++q) {
+        const int64_t n = n0 + c0 + 32 * q + r;
+        const bool nok = n < p.N;
+        const float bv = (EPI == 1 && p.bias != nullptr && nok) ? p.bias[n] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int64_t m = m0 + r0 + 32 * i + 8 * (v >> 2) + 4 * g + (v & 3);
+                if (nok && m < p.M) {
+                    float x = acc[i][q][v];
+                    if (EPI == 1) {
+                        if (p.bias != nullptr) x = x + bv;
+                        x = act_apply(x, p.act);
+                    }
+                    if (EPI == 2)
+                        ((float*)p.C)[m * p.ldc + n] = x;
+                    else
+                        ((unsigned short*)p.C)[m * p.ldc + n] = f32_to_bf16_rne(x);
+                }
+            }
+        }
+    }
+}
+
 }  // namespace
+
+#define C3_GEMM_BF16_PP(NAME, AK, BKC, EPI, BK, ST) \
+    extern "C" __global__ __launch_bounds__(512) void NAME(GemmArgs p) { gemm_bf16_pp_body<AK, BKC, EPI, BK, ST>(p); }
+#define C3_GEMM_BF16_PP_KINDS(T, BK, ST)                                   \
+    C3_GEMM_BF16_PP(c3_gemm_bf16_fwd_##T, true, false, 1, BK, ST)          \
+    C3_GEMM_BF16_PP(c3_gemm_bf16_dx_##T, true, true, 0, BK, ST)            \
+    C3_GEMM_BF16_PP(c3_gemm_bf16_dw_##T, false, false, 2, BK, ST)          \
+    C3_GEMM_BF16_PP(c3_gemm_bf16_dwb_##T, false, false, 0, BK, ST)         \
+    C3_GEMM_BF16_PP(c3_gemm_bf16_tt_##T, false, true, 0, BK, ST)
+
+// d256pp: 32-deep k, 4 stages (128 KiB of LDS).
+C3_GEMM_BF16_PP_KINDS(d256pp, 32, 4)
 
 #define C3_GEMM_BF16_D(NAME, WM, WN, AK, BKC, EPI, BK, ST)                                  \
     extern "C" __global__ __launch_bounds__(64 * WM * WN) void NAME(GemmArgs p) {          \

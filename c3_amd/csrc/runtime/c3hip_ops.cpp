@@ -116,7 +116,7 @@ const Tile* choose_bf16_tile(int64_t M, int64_t N) {
 // backward masks are applied by the pre-pass), K a multiple of the tile's k
 // depth, and a problem of at least 64 output tiles so the large tile fills
 // the chip.
-const Tile kBf16Direct[] = {{"d256w8", 256, 256, 512, 64}, {"d256rq", 256, 256, 256, 64}};
+const Tile kBf16Direct[] = {{"d256w8", 256, 256, 512, 64}, {"d256rq", 256, 256, 256, 64}, {"d256pp", 256, 256, 512, 32}};
 
 bool direct_eligible(Kind kind, const GemmArgs& a, const Tile* t) {
     if (kind == Kind::DxMask || kind == Kind::DwMask || a.db != nullptr) return false;

@@ -288,7 +288,7 @@ def test_bf16_integer_bit_exact(gpu, stream, M, K, Nn, act):
     same_bits(host(db), rb)
 
 
-@pytest.mark.parametrize("tile", ["d256w8", "d256rq", "t64x64", "t128x128", "t256x128", "t256x256"])
+@pytest.mark.parametrize("tile", ["d256w8", "d256rq", "d256pp", "t64x64", "t128x128", "t256x128", "t256x256"])
 def test_every_bf16_tile_bit_exact(gpu, stream, monkeypatch, tile):
     # Each bf16 kernel family forced for the forward and every backward GEMM,
     # on ragged M and N (the 256x256 tiles run 2x2 blocks with partial edges).
@@ -396,3 +396,26 @@ def test_forced_tile_override(gpu, stream):
     Y = empty((M, Nn), dtype=torch.bfloat16)
     N.linear_fwd(N.BF16, ptr(dev_bf16(X)), ptr(dev_bf16(W)), ptr(dev(b)), ptr(Y), M, K, Nn, 1, stream)
     same_bits(host(Y), _bf16_round(rY))
+
+
+@pytest.mark.parametrize("K", [32, 64, 96, 160])
+def test_bf16_pingpong_short_k_bit_exact(gpu, stream, monkeypatch, K):
+    # The ping-pong tile keeps up to four 32-deep k tiles in flight; K of one to
+    # five tiles covers the prologue and drain paths (fewer tiles than stages).
+    from tests.parity import dev_bf16
+
+    monkeypatch.setenv("C3_HIP_GEMM_TILE_BF16", "d256pp")
+    M, Nn = 264, 520
+    X, W, b, dY = ints(95, (M, K)), ints(96, (K, Nn)), ints(97, Nn), ints(98, (M, Nn))
+    Y = empty((M, Nn), dtype=torch.bfloat16)
+    N.linear_fwd(N.BF16, ptr(dev_bf16(X)), ptr(dev_bf16(W)), ptr(dev(b)), ptr(Y), M, K, Nn, 1, stream)
+    rY = _bf16_round(O.linear_fwd(X, W, b, 1))
+    same_bits(host(Y), rY)
+    dX = empty((M, K), dtype=torch.bfloat16)
+    dW, db = empty((K, Nn)), empty(Nn)
+    N.linear_bwd(N.BF16, ptr(dev_bf16(X)), ptr(dev_bf16(W)), ptr(Y), ptr(dev_bf16(dY)), ptr(dX), ptr(dW), ptr(db),
+                 M, K, Nn, 1, stream)
+    rX, rW, rb = O.linear_bwd(X, W, rY, dY, 1)
+    same_bits(host(dX), _bf16_round(rX))
+    same_bits(host(dW), rW)
+    same_bits(host(db), rb)
