@@ -288,7 +288,12 @@ C3_GEMM_BF16_KINDS(t256x256, 256, 256, 2, 2)
 //     ds_read_b128 fragment read touches fall into distinct banks; keying on
 //     r & 7 leaves a 2-way conflict.  Fragment: one ds_read_b128.
 //   RC (row contiguous in global): LDS [BK k][ROWS], the chunk holding rows
-//     8c..8c+7 of k-row kr sits in slot c ^ (2 * (kr % 4)).  Fragment: two
+//     8c..8c+7 of k-row kr sits in slot c ^ (4 * (kr % 4)).  A k-row is
+//     512 bytes, so every k-row starts on bank 0; the 32 lanes of one half of
+//     a transposed read address k-rows kbase..kbase+3 and chunks c0..c0+3,
+//     and the key 4 * (kr % 4) puts those 16 (kr, c) pairs on 16 distinct
+//     16-byte bank groups (no conflict; the key 2 * (kr % 4) left a 2-way
+//     conflict, 2 extra cycles per read in the LDS counters).  Fragment: two
 //     ds_read_b64_tr_b16; in each 16-lane group lane j receives element j%4
 //     of the 8-byte pieces addressed by lanes 4r + j/4 (r = 0..3), so lanes
 //     address k-rows kbase + (j/4) at column offset 4*(j%4) and each lane
@@ -332,7 +337,7 @@ struct DirectTile {
                 goff[i] = (uint32_t)(gr * ld + 8 * c);
             } else {
                 const int kr = q * (64 / RC_CPR) + lane / RC_CPR;
-                const int c = (lane % RC_CPR) ^ (2 * (kr & 3));
+                const int c = (lane % RC_CPR) ^ (4 * (kr & 3));
                 int64_t gc = grow0 + 8 * c;
                 if (gc > rows_total - 8) gc = rows_total - 8;
                 goff[i] = (uint32_t)(kr * ld + gc);
@@ -381,7 +386,7 @@ struct DirectTile {
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 const int kr = 16 * st + 8 * (G >> 1) + 4 * h + (sp >> 2);
-                const int slot = (col >> 3) ^ (2 * (kr & 3));
+                const int slot = (col >> 3) ^ (4 * (kr & 3));
                 v[h] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(S + kr * ROWS + slot * 8 + (col & 7)));
             }
             i16x8 w = {v[0][0], v[0][1], v[0][2], v[0][3], v[1][0], v[1][1], v[1][2], v[1][3]};
@@ -406,7 +411,109 @@ __device__ __forceinline__ void wait_tiles_after(int after) {
     else wait_vmcnt<0>();
 }
 
+// Epilogue of the direct kernels.  Their MFMAs take the B fragment as the
+// first operand, so each 32x32 accumulator block holds C transposed: lane l,
+// register v of block (i, q) is C[mb + 32i + l%32][nb + 32q + 8(v/4) +
+// 4(l/32) + v%4], four consecutive columns per register group.  fp32 output
+// stores those 16 bytes as they are; bf16 output packs them to 8 bytes and
+// v_permlane32_swap trades halves between lanes l and l + 32 so that each
+// lane holds 8 consecutive columns (16 bytes): lanes 0..31 columns 8t..8t+7,
+// lanes 32..63 columns 8(t+1).., for t = 0, 2.  Every store then moves 16
+// bytes per lane.  Columns past N and rows past M are never written; a tile
+// edge, an unaligned C or a leading dimension that breaks 16-byte alignment
+// takes the element-wise path.
 // EPI: 0 store bf16, 1 bias + act then store bf16, 2 store fp32.
+// One 32x32 block: a = its accumulators, m = this lane's row, nq = the
+// block's first column, bv = the bias of this lane's 16 columns.
+template <int EPI>
+__device__ __forceinline__ void store_block_t(const GemmArgs& p, const f32x16& a, int64_t m, int64_t nq,
+                                              const float (&bv)[16], bool vec, int h) {
+    float x[16];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        x[v] = a[v];
+        if (EPI == 1) {
+            if (p.bias != nullptr) x[v] = x[v] + bv[v];
+            x[v] = act_apply(x[v], p.act);
+        }
+    }
+    if (EPI == 2) {
+        float* C = (float*)p.C + m * p.ldc;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int64_t n0 = nq + 8 * t + 4 * h;
+            if (m < p.M) {
+                if (vec && n0 + 4 <= p.N) {
+                    *(f32x4*)(C + n0) = f32x4{x[4 * t], x[4 * t + 1], x[4 * t + 2], x[4 * t + 3]};
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (n0 + e < p.N) C[n0 + e] = x[4 * t + e];
+                }
+            }
+        }
+    } else {
+        uint32_t P[4][2];
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int d = 0; d < 2; ++d)
+                P[t][d] = (uint32_t)f32_to_bf16_rne(x[4 * t + 2 * d]) |
+                          ((uint32_t)f32_to_bf16_rne(x[4 * t + 2 * d + 1]) << 16);
+        unsigned short* C = (unsigned short*)p.C + m * p.ldc;
+#pragma unroll
+        for (int t = 0; t < 4; t += 2) {
+            uint32_t w[4];
+#pragma unroll
+            for (int d = 0; d < 2; ++d) {
+                // Lanes 0..31 keep their own group t and take lane l + 32's;
+                // lanes 32..63 take lane l - 32's group t + 1 and keep their own.
+                const auto r = __builtin_amdgcn_permlane32_swap(P[t][d], P[t + 1][d], false, false);
+                w[d] = r[0];
+                w[2 + d] = r[1];
+            }
+            const int64_t n0 = nq + 8 * (t + h);
+            if (m < p.M) {
+                if (vec && n0 + 8 <= p.N) {
+                    *(u32x4*)(C + n0) = u32x4{w[0], w[1], w[2], w[3]};
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        if (n0 + e < p.N) C[n0 + e] = (unsigned short)(w[e >> 1] >> (16 * (e & 1)));
+                }
+            }
+        }
+    }
+}
+
+// Blocks are visited through template recursion so that every accumulator
+// index is a constant (a loop the compiler declined to unroll would index
+// the array at run time and move it to scratch memory).
+template <int EPI, int FM, int FN, int B>
+__device__ __forceinline__ void store_blocks_t(const GemmArgs& p, f32x16 (&acc)[FM][FN], int64_t mb, int64_t nb,
+                                               bool vec, int lane) {
+    if constexpr (B < FM * FN) {
+        constexpr int q = B / FM, i = B % FM;
+        const int h = lane >> 5;
+        const int64_t nq = nb + 32 * q;
+        float bv[16];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int64_t n = nq + 8 * (v >> 2) + 4 * h + (v & 3);
+            bv[v] = (EPI == 1 && p.bias != nullptr && n < p.N) ? p.bias[n] : 0.0f;
+        }
+        store_block_t<EPI>(p, acc[i][q], mb + 32 * i + (lane & 31), nq, bv, vec, h);
+        store_blocks_t<EPI, FM, FN, B + 1>(p, acc, mb, nb, vec, lane);
+    }
+}
+
+template <int EPI, int FM, int FN>
+__device__ __forceinline__ void store_tile_t(const GemmArgs& p, f32x16 (&acc)[FM][FN], int64_t mb, int64_t nb,
+                                             int lane) {
+    const bool vec = ((uintptr_t)p.C & 15) == 0 && (p.ldc & (EPI == 2 ? 3 : 7)) == 0;
+    store_blocks_t<EPI, FM, FN, 0>(p, acc, mb, nb, vec, lane);
+}
+
 template <int WAVES_M, int WAVES_N, bool AK, bool BKC, int EPI, int BK, int STAGES>
 __device__ __forceinline__ void gemm_bf16_direct_body(const GemmArgs& p) {
     constexpr int BM = 256, BN = 256, NW = WAVES_M * WAVES_N;
@@ -477,35 +584,11 @@ __device__ __forceinline__ void gemm_bf16_direct_body(const GemmArgs& p) {
             for (int i = 0; i < FM; ++i)
 #pragma unroll
                 for (int j = 0; j < FN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
         }
     }
 
-    const int r = lane & 31, g = lane >> 5;
-#pragma unroll
-    for (int j = 0; j < FN; ++j) {
-        const int64_t n = n0 + wn * TN + 32 * j + r;
-        const bool nok = n < p.N;
-        const float bv = (EPI == 1 && p.bias != nullptr && nok) ? p.bias[n] : 0.0f;
-#pragma unroll
-        for (int i = 0; i < FM; ++i) {
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int64_t m = m0 + wm * TM + 32 * i + 8 * (v >> 2) + 4 * g + (v & 3);
-                if (nok && m < p.M) {
-                    float x = acc[i][j][v];
-                    if (EPI == 1) {
-                        if (p.bias != nullptr) x = x + bv;
-                        x = act_apply(x, p.act);
-                    }
-                    if (EPI == 2)
-                        ((float*)p.C)[m * p.ldc + n] = x;
-                    else
-                        ((unsigned short*)p.C)[m * p.ldc + n] = f32_to_bf16_rne(x);
-                }
-            }
-        }
-    }
+    store_tile_t<EPI, FM, FN>(p, acc, m0 + wm * TM, n0 + wn * TN, lane);
 }
 
 
@@ -608,7 +691,7 @@ __device__ __forceinline__ void gemm_bf16_rq_body(const GemmArgs& p) {
 #pragma unroll
             for (int q = 0; q < FM * FN; ++q) {
                 const int i = q / FN, j = q % FN;
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cur][i], fb[cur][j], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[cur][j], fa[cur][i], acc[i][j], 0, 0, 0);
                 __builtin_amdgcn_sched_barrier(0);
                 if (reads && q < FM) fa[nxt][q] = TA::frag(Sr, r0 + 32 * q, sr, lane);
                 if (reads && q >= FM && q < FM + FN) fb[nxt][q - FM] = TB::frag(Sr + A_EL, c0 + 32 * (q - FM), sr, lane);
@@ -623,31 +706,7 @@ __device__ __forceinline__ void gemm_bf16_rq_body(const GemmArgs& p) {
         }
     }
 
-    const int r = lane & 31, g = lane >> 5;
-#pragma unroll
-    for (int j = 0; j < FN; ++j) {
-        const int64_t n = n0 + c0 + 32 * j + r;
-        const bool nok = n < p.N;
-        const float bv = (EPI == 1 && p.bias != nullptr && nok) ? p.bias[n] : 0.0f;
-#pragma unroll
-        for (int i = 0; i < FM; ++i) {
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int64_t m = m0 + r0 + 32 * i + 8 * (v >> 2) + 4 * g + (v & 3);
-                if (nok && m < p.M) {
-                    float x = acc[i][j][v];
-                    if (EPI == 1) {
-                        if (p.bias != nullptr) x = x + bv;
-                        x = act_apply(x, p.act);
-                    }
-                    if (EPI == 2)
-                        ((float*)p.C)[m * p.ldc + n] = x;
-                    else
-                        ((unsigned short*)p.C)[m * p.ldc + n] = f32_to_bf16_rne(x);
-                }
-            }
-        }
-    }
+    store_tile_t<EPI, FM, FN>(p, acc, m0 + r0, n0 + c0, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -753,57 +812,51 @@ __device__ __forceinline__ void gemm_bf16_pp_body(const GemmArgs& p) {
             for (int i = 0; i < FM; ++i)
 #pragma unroll
                 for (int q = 0; q < FN; ++q)
-                    acc[i][q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[s][i], fb[s][q], acc[i][q], 0, 0, 0);
+                    acc[i][q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[s][q], fa[s][i], acc[i][q], 0, 0, 0);
         if (grp == 0) wait_tiles_after<NIW, STAGES - 1>(max(after, 0));
         __builtin_amdgcn_sched_barrier(0);
         if (grp == 0 || j + 1 < nk) __syncthreads();
         __builtin_amdgcn_sched_barrier(0);
     }
 
-    const int r = lane & 31, g = lane >> 5;
-#pragma unroll
-    for (int q = 0; q < FN; ++q) {
-        const int64_t n = n0 + c0 + 32 * q + r;
-        const bool nok = n < p.N;
-        const float bv = (EPI == 1 && p.bias != nullptr && nok) ? p.bias[n] : 0.0f;
-#pragma unroll
-        for (int i = 0; i < FM; ++i) {
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int64_t m = m0 + r0 + 32 * i + 8 * (v >> 2) + 4 * g + (v & 3);
-                if (nok && m < p.M) {
-                    float x = acc[i][q][v];
-                    if (EPI == 1) {
-                        if (p.bias != nullptr) x = x + bv;
-                        x = act_apply(x, p.act);
-                    }
-                    if (EPI == 2)
-                        ((float*)p.C)[m * p.ldc + n] = x;
-                    else
-                        ((unsigned short*)p.C)[m * p.ldc + n] = f32_to_bf16_rne(x);
-                }
-            }
-        }
-    }
+    store_tile_t<EPI, FM, FN>(p, acc, m0 + r0, n0 + c0, lane);
+}
+
+// Split-K: block row blockIdx.y of the grid multiplies k in [y * split_k,
+// y * split_k + split_k) and writes its fp32 partial product to C + y *
+// c_split; c3_splitk_reduce adds the partials.  Only fp32-output kinds split.
+template <bool AK, bool BKC, int EPI>
+__device__ __forceinline__ GemmArgs split_args(const GemmArgs& p) {
+    if (EPI != 2 || p.split_k == 0) return p;
+    GemmArgs q = p;
+    const int64_t k0 = (int64_t)blockIdx.y * p.split_k;
+    q.A = (const unsigned short*)p.A + (AK ? k0 : k0 * p.lda);
+    q.B = (const unsigned short*)p.B + (BKC ? k0 : k0 * p.ldb);
+    q.K = min(p.split_k, p.K - k0);
+    q.C = (float*)p.C + (int64_t)blockIdx.y * p.c_split;
+    return q;
 }
 
 }  // namespace
 
 #define C3_GEMM_BF16_PP(NAME, AK, BKC, EPI, BK, ST) \
-    extern "C" __global__ __launch_bounds__(512) void NAME(GemmArgs p) { gemm_bf16_pp_body<AK, BKC, EPI, BK, ST>(p); }
+    extern "C" __global__ __launch_bounds__(512) void NAME(GemmArgs p) { gemm_bf16_pp_body<AK, BKC, EPI, BK, ST>(split_args<AK, BKC, EPI>(p)); }
 #define C3_GEMM_BF16_PP_KINDS(T, BK, ST)                                   \
     C3_GEMM_BF16_PP(c3_gemm_bf16_fwd_##T, true, false, 1, BK, ST)          \
     C3_GEMM_BF16_PP(c3_gemm_bf16_dx_##T, true, true, 0, BK, ST)            \
     C3_GEMM_BF16_PP(c3_gemm_bf16_dw_##T, false, false, 2, BK, ST)          \
     C3_GEMM_BF16_PP(c3_gemm_bf16_dwb_##T, false, false, 0, BK, ST)         \
-    C3_GEMM_BF16_PP(c3_gemm_bf16_tt_##T, false, true, 0, BK, ST)
+    C3_GEMM_BF16_PP(c3_gemm_bf16_tt_##T, false, true, 0, BK, ST)          \
+    C3_GEMM_BF16_PP(c3_gemm_bf16_fwdf_##T, true, false, 2, BK, ST)        \
+    C3_GEMM_BF16_PP(c3_gemm_bf16_dxf_##T, true, true, 2, BK, ST)          \
+    C3_GEMM_BF16_PP(c3_gemm_bf16_ttf_##T, false, true, 2, BK, ST)
 
 // d256pp: 32-deep k, 4 stages (128 KiB of LDS).
 C3_GEMM_BF16_PP_KINDS(d256pp, 32, 4)
 
 #define C3_GEMM_BF16_D(NAME, WM, WN, AK, BKC, EPI, BK, ST)                                  \
     extern "C" __global__ __launch_bounds__(64 * WM * WN) void NAME(GemmArgs p) {          \
-        gemm_bf16_direct_body<WM, WN, AK, BKC, EPI, BK, ST>(p);                             \
+        gemm_bf16_direct_body<WM, WN, AK, BKC, EPI, BK, ST>(split_args<AK, BKC, EPI>(p));   \
     }
 
 // fwd: X (KC) . W (RC) + bias, act -> bf16.  dx: dZ (KC) . W^T (KC) -> bf16.
@@ -813,7 +866,10 @@ C3_GEMM_BF16_PP_KINDS(d256pp, 32, 4)
     C3_GEMM_BF16_D(c3_gemm_bf16_dx_##T, WM, WN, true, true, 0, BK, ST)           \
     C3_GEMM_BF16_D(c3_gemm_bf16_dw_##T, WM, WN, false, false, 2, BK, ST)         \
     C3_GEMM_BF16_D(c3_gemm_bf16_dwb_##T, WM, WN, false, false, 0, BK, ST)        \
-    C3_GEMM_BF16_D(c3_gemm_bf16_tt_##T, WM, WN, false, true, 0, BK, ST)
+    C3_GEMM_BF16_D(c3_gemm_bf16_tt_##T, WM, WN, false, true, 0, BK, ST)        \
+    C3_GEMM_BF16_D(c3_gemm_bf16_fwdf_##T, WM, WN, true, false, 2, BK, ST)      \
+    C3_GEMM_BF16_D(c3_gemm_bf16_dxf_##T, WM, WN, true, true, 2, BK, ST)        \
+    C3_GEMM_BF16_D(c3_gemm_bf16_ttf_##T, WM, WN, false, true, 2, BK, ST)
 
 // d256w8: 8 waves of 128x64, 64-deep k, 2 stages.
 C3_GEMM_BF16_D_KINDS(d256w8, 2, 4, 64, 2)
@@ -821,13 +877,61 @@ C3_GEMM_BF16_D_KINDS(d256w8, 2, 4, 64, 2)
 
 
 #define C3_GEMM_BF16_RQ(NAME, AK, BKC, EPI, BK, ST) \
-    extern "C" __global__ __launch_bounds__(256) void NAME(GemmArgs p) { gemm_bf16_rq_body<AK, BKC, EPI, BK, ST>(p); }
+    extern "C" __global__ __launch_bounds__(256) void NAME(GemmArgs p) { gemm_bf16_rq_body<AK, BKC, EPI, BK, ST>(split_args<AK, BKC, EPI>(p)); }
 #define C3_GEMM_BF16_RQ_KINDS(T, BK, ST)                                   \
     C3_GEMM_BF16_RQ(c3_gemm_bf16_fwd_##T, true, false, 1, BK, ST)          \
     C3_GEMM_BF16_RQ(c3_gemm_bf16_dx_##T, true, true, 0, BK, ST)            \
     C3_GEMM_BF16_RQ(c3_gemm_bf16_dw_##T, false, false, 2, BK, ST)          \
     C3_GEMM_BF16_RQ(c3_gemm_bf16_dwb_##T, false, false, 0, BK, ST)         \
-    C3_GEMM_BF16_RQ(c3_gemm_bf16_tt_##T, false, true, 0, BK, ST)
+    C3_GEMM_BF16_RQ(c3_gemm_bf16_tt_##T, false, true, 0, BK, ST)          \
+    C3_GEMM_BF16_RQ(c3_gemm_bf16_fwdf_##T, true, false, 2, BK, ST)        \
+    C3_GEMM_BF16_RQ(c3_gemm_bf16_dxf_##T, true, true, 2, BK, ST)          \
+    C3_GEMM_BF16_RQ(c3_gemm_bf16_ttf_##T, false, true, 2, BK, ST)
 
 // d256rq: 64-deep k, 2 stages.
 C3_GEMM_BF16_RQ_KINDS(d256rq, 64, 2)
+
+// Split-K reduction: C[m, n] = epilogue(sum over s of ws[s * slice + m * N + n])
+// with the splits added in order s = 0, 1, ... (deterministic).  Epilogue:
+// + bias[n] (when non-null), act, then bf16 (round to nearest even) or fp32.
+// One thread per 4 consecutive columns of a row.
+struct SplitReduceArgs {
+    const float* ws;
+    void* C;
+    const float* bias;
+    int64_t M, N, ldc, slice;
+    int S, act, out_bf16, _pad;
+};
+
+extern "C" __global__ __launch_bounds__(256) void c3_splitk_reduce(SplitReduceArgs a) {
+    const int64_t vpr = (a.N + 3) / 4;
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t m = t / vpr, n0 = 4 * (t % vpr);
+    if (m >= a.M) return;
+    const float* w = a.ws + m * a.N + n0;
+    float x[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if ((a.N & 3) == 0) {
+        for (int s = 0; s < a.S; ++s) {
+            const f32x4 v = __builtin_nontemporal_load((const f32x4*)(w + (int64_t)s * a.slice));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x[e] += v[e];
+        }
+    } else {
+        for (int s = 0; s < a.S; ++s)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (n0 + e < a.N) x[e] += w[(int64_t)s * a.slice + e];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int64_t n = n0 + e;
+        if (n >= a.N) break;
+        float y = x[e];
+        if (a.bias != nullptr) y = y + a.bias[n];
+        y = act_apply(y, a.act);
+        if (a.out_bf16)
+            ((unsigned short*)a.C)[m * a.ldc + n] = f32_to_bf16_rne(y);
+        else
+            ((float*)a.C)[m * a.ldc + n] = y;
+    }
+}

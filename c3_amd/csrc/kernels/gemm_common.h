@@ -31,6 +31,8 @@ struct GemmArgs {
     int64_t lda, ldb, ldc;
     int act;            // 0: none, 1: ReLU (maxnum(x, 0))
     int _pad;
+    int64_t split_k;    // split-K: k extent of one split (blockIdx.y = split), 0 = none
+    int64_t c_split;    // split-K: elements between the fp32 outputs of consecutive splits
 };
 
 // Blocks are handed to the 8 XCDs round-robin (block i runs on XCD i % 8).

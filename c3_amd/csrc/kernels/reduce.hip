@@ -9,10 +9,15 @@
 // the result is deterministic run to run and within fp32 rounding of the
 // sequential sum.
 //
-// axis 0 is two passes: pass 1 writes one partial row per chunk of rows into
-// a workspace [nchunks, N]; pass 2 adds the partials in chunk order.  Each
-// thread owns one column, so every row access of a wave is 256 contiguous
-// bytes.
+// axis 0 is two passes.  Pass 1 (c3_colsum_partial_f32 and the backward
+// pre-passes) writes one partial row per chunk of rows into a workspace
+// [nchunks, N]; pass 2 (c3_colsum_final_f32) adds the partials.  A pass-1
+// block is `vb` column units (a column, or 8 columns for bf16) by 256 / vb
+// row lanes: a narrow matrix still gives every block 256 busy threads.  Row
+// lane r of a chunk sums rows r, r + 256/vb, ... in order; the lanes are then
+// added in lane order through LDS, so each partial has one fixed order.
+// Consecutive threads read consecutive column units of a row (contiguous
+// bytes per wave).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -20,42 +25,60 @@ constexpr int kThreads = 256;
 
 // mask (nullable, same layout as in): sums (mask > 0 ? 1 : 0) * in, the bias
 // gradient of a ReLU layer computed from its forward output Y and dY.
+// Grid: (ceil(N / vb), nchunks); block 256 = vb columns x (256 / vb) row lanes.
 extern "C" __global__ __launch_bounds__(kThreads) void c3_colsum_partial_f32(
     const float* __restrict__ in, const float* __restrict__ mask, float* __restrict__ part, int64_t M, int64_t N,
-    int64_t rows_per_chunk) {
-    const int64_t j = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    int64_t rows_per_chunk, int vb) {
+    __shared__ float red[kThreads];
+    const int rb = kThreads / vb;
+    const int u = threadIdx.x % vb, rl = threadIdx.x / vb;
+    const int64_t j = (int64_t)blockIdx.x * vb + u;
     const int64_t chunk = blockIdx.y;
-    if (j >= N) return;
     const int64_t r0 = chunk * rows_per_chunk;
     const int64_t r1 = min(M, r0 + rows_per_chunk);
-    // Four independent partial sums for memory-level parallelism, combined in
-    // a fixed order.
-    float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    int64_t i = r0;
-    if (mask) {
-        for (; i + 4 <= r1; i += 4)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int64_t o = (i + q) * N + j;
-                s[q] += (mask[o] > 0.0f ? 1.0f : 0.0f) * in[o];
-            }
-        for (; i < r1; ++i) s[0] += (mask[i * N + j] > 0.0f ? 1.0f : 0.0f) * in[i * N + j];
-    } else {
-        for (; i + 4 <= r1; i += 4)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) s[q] += in[(i + q) * N + j];
-        for (; i < r1; ++i) s[0] += in[i * N + j];
+    float s = 0.0f;
+    if (j < N) {
+        for (int64_t i = r0 + rl; i < r1; i += rb) {
+            const int64_t o = i * N + j;
+            s += mask ? (mask[o] > 0.0f ? 1.0f : 0.0f) * in[o] : in[o];
+        }
     }
-    part[chunk * N + j] = (s[0] + s[1]) + (s[2] + s[3]);
+    if (rb > 1) {
+        red[threadIdx.x] = s;
+        __syncthreads();
+        if (rl == 0)
+            for (int k = 1; k < rb; ++k) s += red[threadIdx.x + k * vb];
+    }
+    if (rl == 0 && j < N) part[chunk * N + j] = s;
 }
 
-extern "C" __global__ __launch_bounds__(kThreads) void c3_colsum_final_f32(
+// Pass 2: out[j] = sum over chunks of part[c][j].  Block: 64 columns x 8
+// waves; wave w adds chunks w, w + 8, ... into four interleaved sums, and the
+// eight wave sums are added in wave order.  Grid: ceil(N / 64).
+extern "C" __global__ __launch_bounds__(512) void c3_colsum_final_f32(
     const float* __restrict__ part, float* __restrict__ out, int64_t nchunks, int64_t N) {
-    const int64_t j = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    if (j >= N) return;
-    float s = 0.0f;
-    for (int64_t c = 0; c < nchunks; ++c) s += part[c * N + j];
-    out[j] = s;
+    __shared__ float red[8][64];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int64_t j = (int64_t)blockIdx.x * 64 + lane;
+    float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+    if (j < N) {
+        int64_t c = w;
+        for (; c + 24 < nchunks; c += 32) {
+            s0 += part[c * N + j];
+            s1 += part[(c + 8) * N + j];
+            s2 += part[(c + 16) * N + j];
+            s3 += part[(c + 24) * N + j];
+        }
+        for (; c < nchunks; c += 8) s0 += part[c * N + j];
+    }
+    red[w][lane] = (s0 + s1) + (s2 + s3);
+    __syncthreads();
+    if (w == 0 && j < N) {
+        float t = red[0][lane];
+#pragma unroll
+        for (int k = 1; k < 8; ++k) t += red[k][lane];
+        out[j] = t;
+    }
 }
 
 // One wave per row.
@@ -95,67 +118,95 @@ __device__ __forceinline__ float act_grad(float y, float d, int act) {
     return d;
 }
 
-// fp32: one thread per column of a chunk of rows (consecutive threads read
-// consecutive columns of a row).
+// fp32: one column per thread, block = vb columns x (256 / vb) row lanes,
+// grid (ceil(N / vb), nchunks).
 extern "C" __global__ __launch_bounds__(kThreads) void c3_dz_colsum_f32(
     const float* __restrict__ Y, const float* __restrict__ dY, float* __restrict__ dZ, float* __restrict__ part,
-    int64_t M, int64_t N, int64_t rows_per_chunk, int act) {
-    const int64_t n = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    if (n >= N) return;
+    int64_t M, int64_t N, int64_t rows_per_chunk, int act, int vb) {
+    __shared__ float red[kThreads];
+    const int rb = kThreads / vb;
+    const int u = threadIdx.x % vb, rl = threadIdx.x / vb;
+    const int64_t n = (int64_t)blockIdx.x * vb + u;
     const int64_t chunk = blockIdx.y;
     const int64_t r0 = chunk * rows_per_chunk;
     const int64_t r1 = min(M, r0 + rows_per_chunk);
     float s = 0.0f;
-    for (int64_t i = r0; i < r1; ++i) {
-        const int64_t off = i * N + n;
-        const float d = act_grad(act ? Y[off] : 0.0f, dY[off], act);
-        if (dZ) dZ[off] = d;
-        s += d;
+    if (n < N) {
+        for (int64_t i = r0 + rl; i < r1; i += rb) {
+            const int64_t off = i * N + n;
+            const float d = act_grad(act ? Y[off] : 0.0f, dY[off], act);
+            if (dZ) dZ[off] = d;
+            s += d;
+        }
     }
-    if (part) part[chunk * N + n] = s;
+    if (part) {
+        if (rb > 1) {
+            red[threadIdx.x] = s;
+            __syncthreads();
+            if (rl == 0)
+                for (int k = 1; k < rb; ++k) s += red[threadIdx.x + k * vb];
+        }
+        if (rl == 0 && n < N) part[chunk * N + n] = s;
+    }
 }
 
-// bf16: one thread owns 8 consecutive columns (a 16-byte vector) of a chunk
-// of rows; consecutive threads cover consecutive vectors of a row.  ReLU
+// bf16: one thread owns 8 consecutive columns (a 16-byte vector); block = vb
+// vectors x (256 / vb) row lanes, grid (ceil(N / 8 / vb), nchunks).  ReLU
 // works on the bit patterns (exact); sigmoid and tanh compute in fp32 and
 // round dZ to bf16 once (nearest even); the column sums add the rounded
 // values the GEMMs then read.  Requires N % 8 == 0 and 16-byte aligned rows.
 extern "C" __global__ __launch_bounds__(kThreads) void c3_dz_colsum_bf16(
     const unsigned short* __restrict__ Y, const unsigned short* __restrict__ dY, unsigned short* __restrict__ dZ,
-    float* __restrict__ part, int64_t M, int64_t N, int64_t rows_per_chunk, int act) {
-    const int64_t v = (int64_t)blockIdx.x * kThreads + threadIdx.x;  // vector index within a row
-    if (8 * v >= N) return;
+    float* __restrict__ part, int64_t M, int64_t N, int64_t rows_per_chunk, int act, int vb) {
+    __shared__ float red[kThreads][9];
+    const int rb = kThreads / vb;
+    const int u = threadIdx.x % vb, rl = threadIdx.x / vb;
+    const int64_t v = (int64_t)blockIdx.x * vb + u;  // vector index within a row
+    const bool active = 8 * v < N;
     const int64_t chunk = blockIdx.y;
     const int64_t r0 = chunk * rows_per_chunk;
     const int64_t r1 = min(M, r0 + rows_per_chunk);
     float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int64_t i = r0; i < r1; ++i) {
-        const int64_t off = i * N + 8 * v;
-        u32x4 d = *(const u32x4*)(dY + off);
-        if (act == 1) {
-            d = mask_mul8(*(const u32x4*)(Y + off), d);
-        } else if (act == 2 || act == 3) {
-            const u32x4 y = *(const u32x4*)(Y + off);
+    if (active) {
+        for (int64_t i = r0 + rl; i < r1; i += rb) {
+            const int64_t off = i * N + 8 * v;
+            u32x4 d = __builtin_nontemporal_load((const u32x4*)(dY + off));
+            if (act == 1) {
+                d = mask_mul8(__builtin_nontemporal_load((const u32x4*)(Y + off)), d);
+            } else if (act == 2 || act == 3) {
+                const u32x4 y = __builtin_nontemporal_load((const u32x4*)(Y + off));
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float lo = act_grad(bf16_to_f32((unsigned short)(y[e] & 0xffff)),
-                                          bf16_to_f32((unsigned short)(d[e] & 0xffff)), act);
-                const float hi = act_grad(bf16_to_f32((unsigned short)(y[e] >> 16)),
-                                          bf16_to_f32((unsigned short)(d[e] >> 16)), act);
-                d[e] = (uint32_t)f32_to_bf16_rne(lo) | ((uint32_t)f32_to_bf16_rne(hi) << 16);
+                for (int e = 0; e < 4; ++e) {
+                    const float lo = act_grad(bf16_to_f32((unsigned short)(y[e] & 0xffff)),
+                                              bf16_to_f32((unsigned short)(d[e] & 0xffff)), act);
+                    const float hi = act_grad(bf16_to_f32((unsigned short)(y[e] >> 16)),
+                                              bf16_to_f32((unsigned short)(d[e] >> 16)), act);
+                    d[e] = (uint32_t)f32_to_bf16_rne(lo) | ((uint32_t)f32_to_bf16_rne(hi) << 16);
+                }
             }
-        }
-        if (dZ) *(u32x4*)(dZ + off) = d;
-        if (part) {
+            if (dZ) *(u32x4*)(dZ + off) = d;
+            if (part) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                s[2 * e] += __uint_as_float(d[e] << 16);
-                s[2 * e + 1] += __uint_as_float(d[e] & 0xffff0000u);
+                for (int e = 0; e < 4; ++e) {
+                    s[2 * e] += __uint_as_float(d[e] << 16);
+                    s[2 * e + 1] += __uint_as_float(d[e] & 0xffff0000u);
+                }
             }
         }
     }
     if (part) {
+        if (rb > 1) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) part[chunk * N + 8 * v + e] = s[e];
+            for (int e = 0; e < 8; ++e) red[threadIdx.x][e] = s[e];
+            __syncthreads();
+            if (rl == 0)
+                for (int k = 1; k < rb; ++k)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) s[e] += red[threadIdx.x + k * vb][e];
+        }
+        if (rl == 0 && active) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) part[chunk * N + 8 * v + e] = s[e];
+        }
     }
 }

@@ -38,6 +38,18 @@ struct GemmArgs {
     int64_t lda, ldb, ldc;
     int act;
     int _pad;
+    int64_t split_k;
+    int64_t c_split;
+};
+
+// Argument block of c3_splitk_reduce (mirrors SplitReduceArgs in
+// c3_amd/csrc/kernels/gemm_bf16.hip).
+struct SplitReduceArgs {
+    const float* ws;
+    void* C;
+    const float* bias;
+    int64_t M, N, ldc, slice;
+    int S, act, out_bf16, _pad;
 };
 
 // Kernel argument block of the fused backward chain (mirrors ChainArgs in

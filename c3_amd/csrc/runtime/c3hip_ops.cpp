@@ -123,24 +123,92 @@ bool direct_eligible(Kind kind, const GemmArgs& a, const Tile* t) {
     return a.K > 0 && a.M >= 8 && a.N >= 8 && a.K % t->bk == 0;
 }
 
+// Split-K plan for a direct tile: a problem with fewer than 64 output tiles
+// of 256x256 and a long k range splits k into S parts (a power of two, each
+// at least 512 deep and a multiple of the tile's k depth, at most 512 blocks
+// and a 256 MiB fp32 workspace in all) when that gives at least 64 blocks;
+// returns 1 for no split.
+int plan_split(const GemmArgs& a, const Tile* t) {
+    const int64_t tiles = ((a.M + 255) / 256) * ((a.N + 255) / 256);
+    if (tiles >= 64) return 1;
+    int S = 1;
+    for (int s = 2; s <= 32; s *= 2) {
+        if (a.K % ((int64_t)s * t->bk) != 0 || a.K / s < 512) break;
+        if (tiles * s > 512) break;
+        if ((double)s * (double)a.M * (double)a.N * 4.0 > (double)(256u << 20)) break;
+        S = s;
+    }
+    return tiles * S >= 64 ? S : 1;
+}
+
 // Sets *unsupported when the calling thread forced a direct tile this
-// problem cannot use.
-const Tile* choose_bf16_direct(Kind kind, const GemmArgs& a, bool* unsupported) {
+// problem cannot use; *split receives the split-K factor (1: none).
+const Tile* choose_bf16_direct(Kind kind, const GemmArgs& a, bool* unsupported, int* split) {
     *unsupported = false;
+    *split = 1;
     if (const char* forced = bf16_forced()) {
         const Tile* t = find_tile(kBf16Direct, sizeof(kBf16Direct) / sizeof(kBf16Direct[0]), forced);
         if (!t) return nullptr;  // a register-staged tile was asked for
-        if (direct_eligible(kind, a, t)) return t;
+        if (direct_eligible(kind, a, t)) {
+            *split = plan_split(a, t);
+            return t;
+        }
         *unsupported = !t_tile_bf16.empty();
         return nullptr;
     }
     if (kind == Kind::DxMask || kind == Kind::DwMask || a.db != nullptr) return nullptr;
     if (a.K == 0) return nullptr;
     if (a.M < 8 || a.N < 8) return nullptr;
-    const int64_t blocks = ((a.M + 255) / 256) * ((a.N + 255) / 256);
-    if (blocks < 64) return nullptr;
     const Tile* t = &kBf16Direct[0];
-    return a.K % t->bk == 0 ? t : nullptr;
+    if (a.K % t->bk != 0) return nullptr;
+    const int64_t blocks = ((a.M + 255) / 256) * ((a.N + 255) / 256);
+    if (blocks >= 64) return t;
+    *split = plan_split(a, t);
+    return *split > 1 ? t : nullptr;
+}
+
+// Split-K run of a plain bf16 GEMM on direct tile d: S block rows write fp32
+// partial products into a stream-ordered workspace [S, M, N]; the reduction
+// adds them in split order and applies the kind's epilogue (forward: bias and
+// activation, bf16 out; dW: fp32 out; the others: bf16 out).
+int run_split(Kind kind, const GemmArgs& a0, const Tile* d, int S, hipStream_t stream) {
+    const char* kn = kind == Kind::Fwd ? "fwdf" : kind == Kind::Dx ? "dxf" : kind == Kind::TT ? "ttf" : "dw";
+    float* ws = nullptr;
+    const int64_t slice = a0.M * a0.N;
+    hipError_t e = hipMallocAsync((void**)&ws, (size_t)S * (size_t)slice * sizeof(float), stream);
+    if (e != hipSuccess) return set_error(C3HIP_ERR_HIP, std::string("hipMallocAsync(split-K): ") + hipGetErrorString(e));
+    GemmArgs g = a0;
+    g.C = ws;
+    g.ldc = a0.N;
+    g.bias = nullptr;
+    g.act = 0;
+    g.split_k = a0.K / S;
+    g.c_split = slice;
+    char name[96];
+    std::snprintf(name, sizeof(name), "c3_gemm_bf16_%s_%s", kn, d->name);
+    const int64_t tiles = ((a0.M + 255) / 256) * ((a0.N + 255) / 256);
+    void* args[] = {&g};
+    int rc = launch(name, dim3((unsigned)tiles, (unsigned)S), dim3(d->threads), args, stream);
+    if (rc == C3HIP_OK) {
+        SplitReduceArgs r{};
+        r.ws = ws;
+        r.C = a0.C;
+        r.bias = kind == Kind::Fwd ? a0.bias : nullptr;
+        r.M = a0.M;
+        r.N = a0.N;
+        r.ldc = a0.ldc;
+        r.slice = slice;
+        r.S = S;
+        r.act = kind == Kind::Fwd ? a0.act : 0;
+        r.out_bf16 = kind == Kind::Dw ? 0 : 1;
+        const int64_t threads = a0.M * ((a0.N + 3) / 4);
+        void* rargs[] = {&r};
+        rc = launch("c3_splitk_reduce", dim3((unsigned)((threads + 255) / 256)), dim3(256), rargs, stream);
+    }
+    e = hipFreeAsync(ws, stream);
+    if (rc == C3HIP_OK && e != hipSuccess)
+        rc = set_error(C3HIP_ERR_HIP, std::string("hipFreeAsync(split-K): ") + hipGetErrorString(e));
+    return rc;
 }
 
 // bf16 kernels always move 16-byte vectors (8 elements): the contiguous
@@ -166,11 +234,13 @@ int run_gemm(int dtype, Kind kind, const GemmArgs& a0, bool a_kc, bool b_kc, hip
             return set_error(C3HIP_ERR_UNSUPPORTED,
                              "bf16 GEMM needs 16-byte aligned operands and contiguous extents that are multiples of 8");
         bool unsupported = false;
-        const Tile* d = choose_bf16_direct(kind, a, &unsupported);
+        int split = 1;
+        const Tile* d = choose_bf16_direct(kind, a, &unsupported, &split);
         if (unsupported)
             return set_error(C3HIP_ERR_UNSUPPORTED, std::string("tile ") + t_tile_bf16 +
                                                         " cannot run this GEMM (masked operand, db side output, "
                                                         "K not a multiple of its k depth, or M or N below 8)");
+        if (d && split > 1) return run_split(kind, a, d, split, stream);
         if (d) {
             char name[96];
             std::snprintf(name, sizeof(name), "c3_gemm_bf16_%s_%s", kind_name(kind), d->name);
@@ -208,31 +278,50 @@ int check_dtype(int dtype) {
     return C3HIP_OK;
 }
 
-// Column sums of (optionally masked) fp32 [M,N] into out[N]: one pass when M
-// is small, else per-chunk partials in a stream-ordered workspace.
+// Launch shape of a column-sum pass over M rows of `units` column units (a
+// column, or an 8-column vector for bf16): blocks of vb units x 256 / vb row
+// lanes, about 256 K threads in all, each adding at least 4 rows.
+struct ColGeom {
+    int vb;
+    unsigned gx;
+    int64_t rows_per_chunk, nchunks;
+};
+
+ColGeom col_geom(int64_t M, int64_t units) {
+    ColGeom g{};
+    g.vb = units > 128 ? 256 : units > 64 ? 128 : 64;
+    const int64_t rb = 256 / g.vb;
+    g.gx = (unsigned)((units + g.vb - 1) / g.vb);
+    const int64_t rows_per_thread = std::max<int64_t>(4, (M * units + (1 << 18) - 1) >> 18);
+    g.rows_per_chunk = std::max<int64_t>(1, rows_per_thread * rb);
+    g.nchunks = std::max<int64_t>(1, (M + g.rows_per_chunk - 1) / g.rows_per_chunk);
+    return g;
+}
+
+// Adds the nchunks partial rows of part [nchunks, N] into out[N].
+int colsum_final(const float* part, float* out, int64_t nchunks, int64_t N, hipStream_t stream) {
+    void* args[] = {(void*)&part, (void*)&out, &nchunks, &N};
+    return launch("c3_colsum_final_f32", dim3((unsigned)((N + 63) / 64)), dim3(512), args, stream);
+}
+
+// Column sums of (optionally masked) fp32 [M,N] into out[N]: one pass when
+// one chunk covers M, else per-chunk partials in a stream-ordered workspace.
 int colsum(const float* in, const float* mask, float* out, int64_t M, int64_t N, hipStream_t stream) {
     if (N == 0) return C3HIP_OK;
-    const int64_t kChunk = 256;
-    int64_t nchunks = (M + kChunk - 1) / kChunk;
-    if (nchunks < 1) nchunks = 1;
-    if (nchunks > 64) nchunks = 64;
-    int64_t rows_per_chunk = (M + nchunks - 1) / nchunks;
-    if (rows_per_chunk < 1) rows_per_chunk = 1;
-    const unsigned gx = (unsigned)((N + 255) / 256);
+    ColGeom g = col_geom(M, N);
+    int64_t rows_per_chunk = g.rows_per_chunk, nchunks = g.nchunks;
+    int vb = g.vb;
     const char* pname = "c3_colsum_partial_f32";
     if (nchunks == 1) {
-        void* args[] = {(void*)&in, (void*)&mask, (void*)&out, &M, &N, &rows_per_chunk};
-        return launch(pname, dim3(gx, 1), dim3(256), args, stream);
+        void* args[] = {(void*)&in, (void*)&mask, (void*)&out, &M, &N, &rows_per_chunk, &vb};
+        return launch(pname, dim3(g.gx, 1), dim3(256), args, stream);
     }
     float* part = nullptr;
     hipError_t e = hipMallocAsync((void**)&part, (size_t)(nchunks * N) * sizeof(float), stream);
     if (e != hipSuccess) return set_error(C3HIP_ERR_HIP, std::string("hipMallocAsync failed: ") + hipGetErrorString(e));
-    void* args1[] = {(void*)&in, (void*)&mask, (void*)&part, &M, &N, &rows_per_chunk};
-    int rc = launch(pname, dim3(gx, (unsigned)nchunks), dim3(256), args1, stream);
-    if (rc == C3HIP_OK) {
-        void* args2[] = {(void*)&part, (void*)&out, &nchunks, &N};
-        rc = launch("c3_colsum_final_f32", dim3(gx), dim3(256), args2, stream);
-    }
+    void* args1[] = {(void*)&in, (void*)&mask, (void*)&part, &M, &N, &rows_per_chunk, &vb};
+    int rc = launch(pname, dim3(g.gx, (unsigned)nchunks), dim3(256), args1, stream);
+    if (rc == C3HIP_OK) rc = colsum_final(part, out, nchunks, N, stream);
     e = hipFreeAsync(part, stream);
     if (rc == C3HIP_OK && e != hipSuccess)
         rc = set_error(C3HIP_ERR_HIP, std::string("hipFreeAsync failed: ") + hipGetErrorString(e));
@@ -266,9 +355,9 @@ int linear_bwd_prepass(int dtype, const void* X, const void* W, const void* Y, c
     if (dtype == C3HIP_BF16 && (N % 8 != 0 || !aligned16(Y) || !aligned16(dY)))
         return set_error(C3HIP_ERR_UNSUPPORTED, "bf16 backward needs N % 8 == 0 and 16-byte aligned Y, dY");
     const bool need_dz = act != C3HIP_ACT_NONE && (dX || dW);
-    int64_t nchunks = std::min<int64_t>(256, std::max<int64_t>(1, (M + 31) / 32));
-    int64_t rows_per_chunk = (M + nchunks - 1) / nchunks;
-    nchunks = (M + rows_per_chunk - 1) / rows_per_chunk;
+    const ColGeom g = col_geom(M, dtype == C3HIP_BF16 ? N / 8 : N);
+    int64_t nchunks = g.nchunks, rows_per_chunk = g.rows_per_chunk;
+    int vb = g.vb;
     void* dz = nullptr;
     float* part = nullptr;
     int rc = C3HIP_OK;
@@ -282,18 +371,10 @@ int linear_bwd_prepass(int dtype, const void* X, const void* W, const void* Y, c
     if (need_dz || db) {
         float* part_out = db ? (nchunks > 1 ? part : db) : nullptr;
         int act_i = act;
-        void* args[] = {(void*)&Y, (void*)&dY, &dz, &part_out, &M, &N, &rows_per_chunk, &act_i};
-        if (dtype == C3HIP_BF16) {
-            const unsigned gx = (unsigned)((N / 8 + 255) / 256);
-            rc = launch("c3_dz_colsum_bf16", dim3(gx, (unsigned)nchunks), dim3(256), args, stream);
-        } else {
-            const unsigned gx = (unsigned)((N + 255) / 256);
-            rc = launch("c3_dz_colsum_f32", dim3(gx, (unsigned)nchunks), dim3(256), args, stream);
-        }
-        if (rc == C3HIP_OK && db && nchunks > 1) {
-            void* args2[] = {(void*)&part, (void*)&db, &nchunks, &N};
-            rc = launch("c3_colsum_final_f32", dim3((unsigned)((N + 255) / 256)), dim3(256), args2, stream);
-        }
+        void* args[] = {(void*)&Y, (void*)&dY, &dz, &part_out, &M, &N, &rows_per_chunk, &act_i, &vb};
+        rc = launch(dtype == C3HIP_BF16 ? "c3_dz_colsum_bf16" : "c3_dz_colsum_f32", dim3(g.gx, (unsigned)nchunks),
+                    dim3(256), args, stream);
+        if (rc == C3HIP_OK && db && nchunks > 1) rc = colsum_final(part, db, nchunks, N, stream);
     }
     const void* dzp = need_dz ? dz : dY;
     if (rc == C3HIP_OK && dX) {

@@ -7,6 +7,7 @@
 // run the same flow on HIP device tensors and are invoked by the GPU pytest.
 #include <unistd.h>
 
+#include <algorithm>
 #include <atomic>
 #include <chrono>
 #include <cstdlib>

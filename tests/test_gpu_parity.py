@@ -240,7 +240,7 @@ def test_matmul_transposes(gpu, stream, ta, tb, M, K, Nn):
 
 
 # --------------------------------------------------------- sum_reduce ----
-@pytest.mark.parametrize("M,Nn", [(1, 1), (100, 37), (5000, 300), (8192, 4096)])
+@pytest.mark.parametrize("M,Nn", [(1, 1), (100, 37), (5000, 300), (8192, 4096), (65536, 8), (20000, 100)])
 @pytest.mark.parametrize("axis", [0, 1])
 def test_sum_reduce(gpu, stream, M, Nn, axis):
     x = ints(71, (M, Nn), -50, 50)
@@ -419,3 +419,57 @@ def test_bf16_pingpong_short_k_bit_exact(gpu, stream, monkeypatch, K):
     same_bits(host(dX), _bf16_round(rX))
     same_bits(host(dW), rW)
     same_bits(host(db), rb)
+
+
+# Split-K: a GEMM with fewer than 64 output tiles of 256x256 and a long k
+# range runs as k splits with fp32 partials added by c3_splitk_reduce.  Each
+# shape splits one GEMM of the layer: (576, 8192, 576) the forward,
+# (576, 576, 8192) dX (k = N), (8192, 576, 576) dW (k = M); 576 = 9 x 64, so
+# every forced direct tile runs all three GEMMs.
+@pytest.mark.parametrize("tile", [None, "d256w8", "d256rq", "d256pp"])
+@pytest.mark.parametrize("M,K,Nn", [(576, 8192, 576), (576, 576, 8192), (8192, 576, 576)])
+def test_bf16_split_k_bit_exact(gpu, stream, monkeypatch, tile, M, K, Nn):
+    from tests.parity import dev_bf16
+
+    if tile is None:
+        monkeypatch.delenv("C3_HIP_GEMM_TILE_BF16", raising=False)
+    else:
+        monkeypatch.setenv("C3_HIP_GEMM_TILE_BF16", tile)
+    X, W, b, dY = ints(101, (M, K)), ints(102, (K, Nn)), ints(103, Nn), ints(104, (M, Nn))
+    Y = empty((M, Nn), dtype=torch.bfloat16)
+    N.linear_fwd(N.BF16, ptr(dev_bf16(X)), ptr(dev_bf16(W)), ptr(dev(b)), ptr(Y), M, K, Nn, 1, stream)
+    # Integer-valued inputs: every partial sum is an integer below 2^24, so
+    # float64 products in any order are exact and equal the oracle's
+    # sequential loop (checked against it in test_oracle); this keeps the
+    # reference fast at k = 8192.
+    X64, W64, dY64 = X.astype(np.float64), W.astype(np.float64), dY.astype(np.float64)
+    rY = _bf16_round(np.maximum(X64 @ W64 + b, 0.0).astype(np.float32))
+    same_bits(host(Y), rY)
+    dX = empty((M, K), dtype=torch.bfloat16)
+    dW, db = empty((K, Nn)), empty(Nn)
+    N.linear_bwd(N.BF16, ptr(dev_bf16(X)), ptr(dev_bf16(W)), ptr(Y), ptr(dev_bf16(dY)), ptr(dX), ptr(dW), ptr(db),
+                 M, K, Nn, 1, stream)
+    dZ = np.where(rY > 0, dY64, 0.0)
+    same_bits(host(dX), _bf16_round((dZ @ W64.T).astype(np.float32)))
+    same_bits(host(dW), (X64.T @ dZ).astype(np.float32))
+    same_bits(host(db), dZ.sum(axis=0).astype(np.float32))
+
+
+def test_bf16_split_k_real_values(gpu, stream):
+    # Real-valued inputs through the split forward and split dW: the split
+    # order differs from the sequential k loop only by rounding.
+    from tests.parity import dev_bf16
+
+    M, K, Nn = 576, 8192, 576
+    X = _bf16_round(O.normal(111, (M, K)))
+    W = _bf16_round(O.normal(112, (K, Nn), 0.0, 1.0 / np.sqrt(K)))
+    b = O.normal(113, Nn, 0.0, 0.1)
+    Y = empty((M, Nn), dtype=torch.bfloat16)
+    N.linear_fwd(N.BF16, ptr(dev_bf16(X)), ptr(dev_bf16(W)), ptr(dev(b)), ptr(Y), M, K, Nn, 1, stream)
+    t = O.matmul(X, W)
+    rY = O.bias_act(t, b, 1)
+    z = O.bias_act(t, b, 0)
+    gY = host(Y)
+    bound = gemm_bound(X, W, K)
+    assert_close_gemm(gY, rY, bound, BF16_TOL, out_round=2.0 ** -8, what="Y bf16 split")
+    mask_flips(gY, z, bound + 2.0 ** -8 * np.abs(z))
