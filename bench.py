@@ -312,10 +312,11 @@ def bench_backward_chain(torch, C, dev, s, n=1 << 26, iters=10):
 SWEEP = [(m, k, n) for m in (1024, 4096, 16384) for k in (1024, 4096, 8192) for n in (1024, 4096, 8192)]
 
 
-def bench_bf16_sweep(torch, C, dev, s, reps=5):
+def bench_bf16_sweep(torch, C, dev, s, reps=5, groups=3, warmup=3):
     """bf16 Linear+bias+ReLU forward + fused backward over the M x K x N sweep
     {1024, 4096, 16384} x {1024, 4096, 8192} x {1024, 4096, 8192}: TFLOP/s of
-    the step (6 M N K flop) per shape, events around `reps` back-to-back steps."""
+    the step (6 M N K flop) per shape, after `warmup` steps: the median over
+    `groups` groups of events around `reps` back-to-back steps."""
     g = torch.Generator(device=dev)
     g.manual_seed(0x5EE9)
     res = {}
@@ -334,15 +335,19 @@ def bench_bf16_sweep(torch, C, dev, s, reps=5):
             C.linear_bwd(C.BF16, X.data_ptr(), W.data_ptr(), Y.data_ptr(), dY.data_ptr(), dX.data_ptr(),
                          dW.data_ptr(), db.data_ptr(), m, k, n, C.ACT_RELU, s)
 
-        step()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        e0.record()
-        for _ in range(reps):
+        for _ in range(warmup):
             step()
-        e1.record()
-        torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1) / reps
+        times = []
+        for _ in range(groups):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            e0.record()
+            for _ in range(reps):
+                step()
+            e1.record()
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1) / reps)
+        ms = sorted(times)[len(times) // 2]
         res[f"{m}x{k}x{n}"] = round(6.0 * m * n * k / (ms * 1e-3) / 1e12, 1)
         del X, W, b, dY, Y, dX, dW, db
     torch.cuda.empty_cache()

@@ -276,8 +276,9 @@ C3_GEMM_BF16_KINDS(t256x128, 256, 128, 2, 2)
 C3_GEMM_BF16_KINDS(t256x256, 256, 256, 2, 2)
 
 // ===========================================================================
-// Direct-to-LDS kernels: 256x256 block tiles, BK-deep k tiles in STAGES LDS
-// stages, 8 waves of 128x64 (2x4) or 4 waves of 128x128 (2x2).
+// Direct-to-LDS kernels: 256x256 block tiles (8 waves of 128x64, 4 waves of
+// 128x128, or 8 ping-pong waves) or 128x128 tiles (4 waves of 64x64),
+// BK-deep k tiles in STAGES LDS stages.
 // Global tiles go straight into LDS with global_load_lds_dwordx4 (lane l's
 // 16 bytes land at base + 16*l of the instruction's 1 KiB), so no staging
 // registers and no LDS stores are needed.  Layouts, per operand:
@@ -514,9 +515,9 @@ __device__ __forceinline__ void store_tile_t(const GemmArgs& p, f32x16 (&acc)[FM
     store_blocks_t<EPI, FM, FN, 0>(p, acc, mb, nb, vec, lane);
 }
 
-template <int WAVES_M, int WAVES_N, bool AK, bool BKC, int EPI, int BK, int STAGES>
+template <int WAVES_M, int WAVES_N, bool AK, bool BKC, int EPI, int BK, int STAGES, int BT>
 __device__ __forceinline__ void gemm_bf16_direct_body(const GemmArgs& p) {
-    constexpr int BM = 256, BN = 256, NW = WAVES_M * WAVES_N;
+    constexpr int BM = BT, BN = BT, NW = WAVES_M * WAVES_N;
     constexpr int TM = BM / WAVES_M, TN = BN / WAVES_N, FM = TM / 32, FN = TN / 32;
     constexpr int PF = STAGES - 1;  // tiles in flight ahead of the one multiplied
     using TA = DirectTile<BM, AK, NW, BK>;
@@ -854,25 +855,29 @@ __device__ __forceinline__ GemmArgs split_args(const GemmArgs& p) {
 // d256pp: 32-deep k, 4 stages (128 KiB of LDS).
 C3_GEMM_BF16_PP_KINDS(d256pp, 32, 4)
 
-#define C3_GEMM_BF16_D(NAME, WM, WN, AK, BKC, EPI, BK, ST)                                  \
-    extern "C" __global__ __launch_bounds__(64 * WM * WN) void NAME(GemmArgs p) {          \
-        gemm_bf16_direct_body<WM, WN, AK, BKC, EPI, BK, ST>(split_args<AK, BKC, EPI>(p));   \
+#define C3_GEMM_BF16_D(NAME, WM, WN, AK, BKC, EPI, BK, ST, BT)                                  \
+    extern "C" __global__ __launch_bounds__(64 * WM * WN) void NAME(GemmArgs p) {              \
+        gemm_bf16_direct_body<WM, WN, AK, BKC, EPI, BK, ST, BT>(split_args<AK, BKC, EPI>(p));   \
     }
 
 // fwd: X (KC) . W (RC) + bias, act -> bf16.  dx: dZ (KC) . W^T (KC) -> bf16.
 // dw: X^T (RC) . dZ (RC) -> fp32.  dwb: same, bf16 out.  tt: A^T (RC) . B^T (KC) -> bf16.
-#define C3_GEMM_BF16_D_KINDS(T, WM, WN, BK, ST)                                  \
-    C3_GEMM_BF16_D(c3_gemm_bf16_fwd_##T, WM, WN, true, false, 1, BK, ST)         \
-    C3_GEMM_BF16_D(c3_gemm_bf16_dx_##T, WM, WN, true, true, 0, BK, ST)           \
-    C3_GEMM_BF16_D(c3_gemm_bf16_dw_##T, WM, WN, false, false, 2, BK, ST)         \
-    C3_GEMM_BF16_D(c3_gemm_bf16_dwb_##T, WM, WN, false, false, 0, BK, ST)        \
-    C3_GEMM_BF16_D(c3_gemm_bf16_tt_##T, WM, WN, false, true, 0, BK, ST)        \
-    C3_GEMM_BF16_D(c3_gemm_bf16_fwdf_##T, WM, WN, true, false, 2, BK, ST)      \
-    C3_GEMM_BF16_D(c3_gemm_bf16_dxf_##T, WM, WN, true, true, 2, BK, ST)        \
-    C3_GEMM_BF16_D(c3_gemm_bf16_ttf_##T, WM, WN, false, true, 2, BK, ST)
+#define C3_GEMM_BF16_D_KINDS(T, WM, WN, BK, ST, BT)                                  \
+    C3_GEMM_BF16_D(c3_gemm_bf16_fwd_##T, WM, WN, true, false, 1, BK, ST, BT)         \
+    C3_GEMM_BF16_D(c3_gemm_bf16_dx_##T, WM, WN, true, true, 0, BK, ST, BT)           \
+    C3_GEMM_BF16_D(c3_gemm_bf16_dw_##T, WM, WN, false, false, 2, BK, ST, BT)         \
+    C3_GEMM_BF16_D(c3_gemm_bf16_dwb_##T, WM, WN, false, false, 0, BK, ST, BT)        \
+    C3_GEMM_BF16_D(c3_gemm_bf16_tt_##T, WM, WN, false, true, 0, BK, ST, BT)        \
+    C3_GEMM_BF16_D(c3_gemm_bf16_fwdf_##T, WM, WN, true, false, 2, BK, ST, BT)      \
+    C3_GEMM_BF16_D(c3_gemm_bf16_dxf_##T, WM, WN, true, true, 2, BK, ST, BT)        \
+    C3_GEMM_BF16_D(c3_gemm_bf16_ttf_##T, WM, WN, false, true, 2, BK, ST, BT)
 
-// d256w8: 8 waves of 128x64, 64-deep k, 2 stages.
-C3_GEMM_BF16_D_KINDS(d256w8, 2, 4, 64, 2)
+// d256w8: 256x256 tiles, 8 waves of 128x64, 64-deep k, 2 stages (128 KiB LDS).
+C3_GEMM_BF16_D_KINDS(d256w8, 2, 4, 64, 2, 256)
+// d128w4: 128x128 tiles, 4 waves of 64x64, 64-deep k, 2 stages (64 KiB LDS,
+// two blocks per CU): four times the blocks of d256w8 for grids too small to
+// fill the chip with 256x256 tiles.
+C3_GEMM_BF16_D_KINDS(d128w4, 2, 2, 64, 2, 128)
 
 
 

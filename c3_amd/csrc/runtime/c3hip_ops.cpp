@@ -116,41 +116,59 @@ const Tile* choose_bf16_tile(int64_t M, int64_t N) {
 // backward masks are applied by the pre-pass), K a multiple of the tile's k
 // depth, and a problem of at least 64 output tiles so the large tile fills
 // the chip.
-const Tile kBf16Direct[] = {{"d256w8", 256, 256, 512, 64}, {"d256rq", 256, 256, 256, 64}, {"d256pp", 256, 256, 512, 32}};
+const Tile kBf16Direct[] = {{"d256w8", 256, 256, 512, 64},
+                             {"d256rq", 256, 256, 256, 64},
+                             {"d256pp", 256, 256, 512, 32},
+                             {"d128w4", 128, 128, 256, 64}};
 
 bool direct_eligible(Kind kind, const GemmArgs& a, const Tile* t) {
     if (kind == Kind::DxMask || kind == Kind::DwMask || a.db != nullptr) return false;
     return a.K > 0 && a.M >= 8 && a.N >= 8 && a.K % t->bk == 0;
 }
 
-// Split-K plan for a direct tile: a problem with fewer than 64 output tiles
-// of 256x256 and a long k range splits k into S parts (a power of two, each
-// at least 512 deep and a multiple of the tile's k depth, at most 512 blocks
-// and a 256 MiB fp32 workspace in all) when that gives at least 64 blocks;
-// returns 1 for no split.
-int plan_split(const GemmArgs& a, const Tile* t) {
-    const int64_t tiles = ((a.M + 255) / 256) * ((a.N + 255) / 256);
-    if (tiles >= 64) return 1;
+int64_t tile_count(const GemmArgs& a, const Tile* t) { return ((a.M + t->bm - 1) / t->bm) * ((a.N + t->bn - 1) / t->bn); }
+
+// Split-K factor for direct tile t: the largest power of two S <= 32 with
+// tiles * S <= max_blocks, each split at least min_k deep and a multiple of
+// the tile's k depth, and an fp32 workspace of at most 256 MiB; 1 = no split.
+int plan_split(const GemmArgs& a, const Tile* t, int64_t max_blocks, int64_t min_k) {
+    const int64_t tiles = tile_count(a, t);
     int S = 1;
     for (int s = 2; s <= 32; s *= 2) {
-        if (a.K % ((int64_t)s * t->bk) != 0 || a.K / s < 512) break;
-        if (tiles * s > 512) break;
+        if (a.K % ((int64_t)s * t->bk) != 0 || a.K / s < min_k) break;
+        if (tiles * s > max_blocks) break;
         if ((double)s * (double)a.M * (double)a.N * 4.0 > (double)(256u << 20)) break;
         S = s;
     }
-    return tiles * S >= 64 ? S : 1;
+    return S;
+}
+
+// Split plan of a forced direct tile: as the size heuristic would split it
+// (fewer tiles than one block per CU), else 1.
+int forced_split(const GemmArgs& a, const Tile* t) {
+    const bool small = t->bm == 128;
+    const int64_t per_wave = small ? 512 : 256;  // blocks resident at once (two 128x128 blocks per CU)
+    if (tile_count(a, t) >= per_wave / 2) return 1;
+    return plan_split(a, t, per_wave, small ? 256 : 512);
 }
 
 // Sets *unsupported when the calling thread forced a direct tile this
 // problem cannot use; *split receives the split-K factor (1: none).
+// Size heuristic (measured on MI355X over the 1024..16384 sweep shapes):
+// 256x256 tiles when they give at least 256 blocks (one per CU); else 128x128 tiles (split
+// into parts at least 512 deep up to 512 blocks, two per CU, when they give
+// fewer than 256 blocks) when they give 128 blocks by themselves or, for
+// K >= 2048, with the split; else the
+// register-staged kernels (best for a 1024^3-sized problem).
 const Tile* choose_bf16_direct(Kind kind, const GemmArgs& a, bool* unsupported, int* split) {
     *unsupported = false;
     *split = 1;
+    const size_t nd = sizeof(kBf16Direct) / sizeof(kBf16Direct[0]);
     if (const char* forced = bf16_forced()) {
-        const Tile* t = find_tile(kBf16Direct, sizeof(kBf16Direct) / sizeof(kBf16Direct[0]), forced);
+        const Tile* t = find_tile(kBf16Direct, nd, forced);
         if (!t) return nullptr;  // a register-staged tile was asked for
         if (direct_eligible(kind, a, t)) {
-            *split = plan_split(a, t);
+            *split = forced_split(a, t);
             return t;
         }
         *unsupported = !t_tile_bf16.empty();
@@ -159,12 +177,17 @@ const Tile* choose_bf16_direct(Kind kind, const GemmArgs& a, bool* unsupported, 
     if (kind == Kind::DxMask || kind == Kind::DwMask || a.db != nullptr) return nullptr;
     if (a.K == 0) return nullptr;
     if (a.M < 8 || a.N < 8) return nullptr;
-    const Tile* t = &kBf16Direct[0];
-    if (a.K % t->bk != 0) return nullptr;
-    const int64_t blocks = ((a.M + 255) / 256) * ((a.N + 255) / 256);
-    if (blocks >= 64) return t;
-    *split = plan_split(a, t);
-    return *split > 1 ? t : nullptr;
+    const Tile* big = find_tile(kBf16Direct, nd, "d256w8");
+    const Tile* small = find_tile(kBf16Direct, nd, "d128w4");
+    if (a.K % big->bk != 0) return nullptr;
+    if (tile_count(a, big) >= 256) return big;
+    const int64_t tiles_s = tile_count(a, small);
+    const int Ss = tiles_s >= 256 ? 1 : plan_split(a, small, 512, 512);  // 256 blocks: one per CU already
+    if (tiles_s >= 128 || (a.K >= 2048 && tiles_s * Ss >= 128)) {
+        *split = Ss;
+        return small;
+    }
+    return nullptr;
 }
 
 // Split-K run of a plain bf16 GEMM on direct tile d: S block rows write fp32
@@ -186,7 +209,7 @@ int run_split(Kind kind, const GemmArgs& a0, const Tile* d, int S, hipStream_t s
     g.c_split = slice;
     char name[96];
     std::snprintf(name, sizeof(name), "c3_gemm_bf16_%s_%s", kn, d->name);
-    const int64_t tiles = ((a0.M + 255) / 256) * ((a0.N + 255) / 256);
+    const int64_t tiles = tile_count(a0, d);
     void* args[] = {&g};
     int rc = launch(name, dim3((unsigned)tiles, (unsigned)S), dim3(d->threads), args, stream);
     if (rc == C3HIP_OK) {
@@ -244,7 +267,7 @@ int run_gemm(int dtype, Kind kind, const GemmArgs& a0, bool a_kc, bool b_kc, hip
         if (d) {
             char name[96];
             std::snprintf(name, sizeof(name), "c3_gemm_bf16_%s_%s", kind_name(kind), d->name);
-            const int64_t blocks = ((a.M + 255) / 256) * ((a.N + 255) / 256);
+            const int64_t blocks = tile_count(a, d);
             void* args[] = {&a};
             return launch(name, dim3((unsigned)blocks), dim3(d->threads), args, stream);
         }

@@ -102,6 +102,18 @@ int load_device(int device, DeviceState** out) {
             ds->module_names.push_back(name);
         }
         ds->dir_scanned = true;
+        // Workspaces (split-K partials, backward pre-pass buffers) come from
+        // the device's default stream-ordered pool; keep freed blocks in the
+        // pool across synchronizations instead of returning them to the
+        // driver, so a repeated call reuses its workspace without remapping.
+        hipMemPool_t pool = nullptr;
+        if (hipDeviceGetDefaultMemPool(&pool, device) == hipSuccess && pool != nullptr) {
+            uint64_t keep = UINT64_MAX;
+            if (hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep) != hipSuccess)
+                (void)hipGetLastError();
+        } else {
+            (void)hipGetLastError();
+        }
     }
     *out = ds;
     return C3HIP_OK;

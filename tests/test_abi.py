@@ -131,7 +131,7 @@ def test_backward_chain_validation():
 
 def test_gemm_tile_override_validation():
     assert native.gemm_tile_names(native.F32) == ["t64x64", "t128x128", "t256x128"]
-    assert native.gemm_tile_names(native.BF16) == ["t64x64", "t128x128", "t256x128", "t256x256", "d256w8", "d256rq", "d256pp"]
+    assert native.gemm_tile_names(native.BF16) == ["t64x64", "t128x128", "t256x128", "t256x256", "d256w8", "d256rq", "d256pp", "d128w4"]
     L = native.load()
     assert L.c3hip_set_gemm_tile(native.F32, b"d256w8") == native.ERR_INVALID  # a bf16-only tile
     assert L.c3hip_set_gemm_tile(native.BF16, b"t32x32") == native.ERR_INVALID

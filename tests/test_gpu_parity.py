@@ -288,7 +288,7 @@ def test_bf16_integer_bit_exact(gpu, stream, M, K, Nn, act):
     same_bits(host(db), rb)
 
 
-@pytest.mark.parametrize("tile", ["d256w8", "d256rq", "d256pp", "t64x64", "t128x128", "t256x128", "t256x256"])
+@pytest.mark.parametrize("tile", ["d256w8", "d256rq", "d256pp", "d128w4", "t64x64", "t128x128", "t256x128", "t256x256"])
 def test_every_bf16_tile_bit_exact(gpu, stream, monkeypatch, tile):
     # Each bf16 kernel family forced for the forward and every backward GEMM,
     # on ragged M and N (the 256x256 tiles run 2x2 blocks with partial edges).
@@ -383,7 +383,7 @@ def test_forced_tile_override(gpu, stream):
             N.set_gemm_tile(N.BF16, tile)
             Y = empty((M, Nn), dtype=torch.bfloat16)
             args = (N.BF16, ptr(dev_bf16(X)), ptr(dev_bf16(W)), ptr(dev(b)), ptr(Y), M, K, Nn, 1, stream)
-            if tile.startswith("d256"):  # K = 264 is not a multiple of the 64-deep k tile
+            if tile.startswith("d"):  # direct tiles: K = 264 is not a multiple of their 32/64-deep k tile
                 with pytest.raises(N.C3HipError) as e:
                     N.linear_fwd(*args)
                 assert e.value.code == N.ERR_UNSUPPORTED
@@ -426,7 +426,7 @@ def test_bf16_pingpong_short_k_bit_exact(gpu, stream, monkeypatch, K):
 # shape splits one GEMM of the layer: (576, 8192, 576) the forward,
 # (576, 576, 8192) dX (k = N), (8192, 576, 576) dW (k = M); 576 = 9 x 64, so
 # every forced direct tile runs all three GEMMs.
-@pytest.mark.parametrize("tile", [None, "d256w8", "d256rq", "d256pp"])
+@pytest.mark.parametrize("tile", [None, "d256w8", "d256rq", "d256pp", "d128w4"])
 @pytest.mark.parametrize("M,K,Nn", [(576, 8192, 576), (576, 576, 8192), (8192, 576, 576)])
 def test_bf16_split_k_bit_exact(gpu, stream, monkeypatch, tile, M, K, Nn):
     from tests.parity import dev_bf16
