@@ -228,28 +228,31 @@ __device__ __forceinline__ void gemm_bf16_body(const GemmArgs& p) {
         }
     }
 
+    with_act(p.act, [&](auto at) {
+        constexpr int ACT = decltype(at)::value;
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-        const int64_t n = n0 + wn * TN + 32 * j + r;
-        const bool nok = n < p.N;
-        const float bv = (p.bias != nullptr && nok) ? p.bias[n] : 0.0f;
+        for (int j = 0; j < FN; ++j) {
+            const int64_t n = n0 + wn * TN + 32 * j + r;
+            const bool nok = n < p.N;
+            const float bv = (p.bias != nullptr && nok) ? p.bias[n] : 0.0f;
 #pragma unroll
-        for (int i = 0; i < FM; ++i) {
+            for (int i = 0; i < FM; ++i) {
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int64_t m = m0 + wm * TM + 32 * i + 8 * (v >> 2) + 4 * g + (v & 3);
-                if (nok && m < p.M) {
-                    float x = acc[i][j][v];
-                    if (p.bias != nullptr) x = x + bv;
-                    x = act_apply(x, p.act);
-                    if (OUT_BF16)
-                        ((unsigned short*)p.C)[m * p.ldc + n] = f32_to_bf16_rne(x);
-                    else
-                        ((float*)p.C)[m * p.ldc + n] = x;
+                for (int v = 0; v < 16; ++v) {
+                    const int64_t m = m0 + wm * TM + 32 * i + 8 * (v >> 2) + 4 * g + (v & 3);
+                    if (nok && m < p.M) {
+                        float x = acc[i][j][v];
+                        if (p.bias != nullptr) x = x + bv;
+                        x = act_c<ACT>(x);
+                        if (OUT_BF16)
+                            ((unsigned short*)p.C)[m * p.ldc + n] = f32_to_bf16_rne(x);
+                        else
+                            ((float*)p.C)[m * p.ldc + n] = x;
+                    }
                 }
             }
         }
-    }
+    });
 }
 
 }  // namespace
@@ -426,7 +429,7 @@ __device__ __forceinline__ void wait_tiles_after(int after) {
 // EPI: 0 store bf16, 1 bias + act then store bf16, 2 store fp32.
 // One 32x32 block: a = its accumulators, m = this lane's row, nq = the
 // block's first column, bv = the bias of this lane's 16 columns.
-template <int EPI>
+template <int EPI, int ACT>
 __device__ __forceinline__ void store_block_t(const GemmArgs& p, const f32x16& a, int64_t m, int64_t nq,
                                               const float (&bv)[16], bool vec, int h) {
     float x[16];
@@ -435,7 +438,7 @@ __device__ __forceinline__ void store_block_t(const GemmArgs& p, const f32x16& a
         x[v] = a[v];
         if (EPI == 1) {
             if (p.bias != nullptr) x[v] = x[v] + bv[v];
-            x[v] = act_apply(x[v], p.act);
+            x[v] = act_c<ACT>(x[v]);
         }
     }
     if (EPI == 2) {
@@ -490,7 +493,7 @@ __device__ __forceinline__ void store_block_t(const GemmArgs& p, const f32x16& a
 // Blocks are visited through template recursion so that every accumulator
 // index is a constant (a loop the compiler declined to unroll would index
 // the array at run time and move it to scratch memory).
-template <int EPI, int FM, int FN, int B>
+template <int EPI, int ACT, int FM, int FN, int B>
 __device__ __forceinline__ void store_blocks_t(const GemmArgs& p, f32x16 (&acc)[FM][FN], int64_t mb, int64_t nb,
                                                bool vec, int lane) {
     if constexpr (B < FM * FN) {
@@ -503,8 +506,8 @@ __device__ __forceinline__ void store_blocks_t(const GemmArgs& p, f32x16 (&acc)[
             const int64_t n = nq + 8 * (v >> 2) + 4 * h + (v & 3);
             bv[v] = (EPI == 1 && p.bias != nullptr && n < p.N) ? p.bias[n] : 0.0f;
         }
-        store_block_t<EPI>(p, acc[i][q], mb + 32 * i + (lane & 31), nq, bv, vec, h);
-        store_blocks_t<EPI, FM, FN, B + 1>(p, acc, mb, nb, vec, lane);
+        store_block_t<EPI, ACT>(p, acc[i][q], mb + 32 * i + (lane & 31), nq, bv, vec, h);
+        store_blocks_t<EPI, ACT, FM, FN, B + 1>(p, acc, mb, nb, vec, lane);
     }
 }
 
@@ -512,7 +515,10 @@ template <int EPI, int FM, int FN>
 __device__ __forceinline__ void store_tile_t(const GemmArgs& p, f32x16 (&acc)[FM][FN], int64_t mb, int64_t nb,
                                              int lane) {
     const bool vec = ((uintptr_t)p.C & 15) == 0 && (p.ldc & (EPI == 2 ? 3 : 7)) == 0;
-    store_blocks_t<EPI, FM, FN, 0>(p, acc, mb, nb, vec, lane);
+    if (EPI == 1)
+        with_act(p.act, [&](auto at) { store_blocks_t<EPI, decltype(at)::value, FM, FN, 0>(p, acc, mb, nb, vec, lane); });
+    else
+        store_blocks_t<EPI, 0, FM, FN, 0>(p, acc, mb, nb, vec, lane);
 }
 
 template <int WAVES_M, int WAVES_N, bool AK, bool BKC, int EPI, int BK, int STAGES, int BT>
@@ -848,6 +854,7 @@ __device__ __forceinline__ GemmArgs split_args(const GemmArgs& p) {
     C3_GEMM_BF16_PP(c3_gemm_bf16_dw_##T, false, false, 2, BK, ST)          \
     C3_GEMM_BF16_PP(c3_gemm_bf16_dwb_##T, false, false, 0, BK, ST)         \
     C3_GEMM_BF16_PP(c3_gemm_bf16_tt_##T, false, true, 0, BK, ST)          \
+    C3_GEMM_BF16_PP(c3_gemm_bf16_fwdt_##T, true, true, 1, BK, ST)         \
     C3_GEMM_BF16_PP(c3_gemm_bf16_fwdf_##T, true, false, 2, BK, ST)        \
     C3_GEMM_BF16_PP(c3_gemm_bf16_dxf_##T, true, true, 2, BK, ST)          \
     C3_GEMM_BF16_PP(c3_gemm_bf16_ttf_##T, false, true, 2, BK, ST)
@@ -860,7 +867,8 @@ C3_GEMM_BF16_PP_KINDS(d256pp, 32, 4)
         gemm_bf16_direct_body<WM, WN, AK, BKC, EPI, BK, ST, BT>(split_args<AK, BKC, EPI>(p));   \
     }
 
-// fwd: X (KC) . W (RC) + bias, act -> bf16.  dx: dZ (KC) . W^T (KC) -> bf16.
+// fwd: X (KC) . W (RC) + bias, act -> bf16.  fwdt: the same with W given
+// transposed ([N, K], KC).  dx: dZ (KC) . W^T (KC) -> bf16.
 // dw: X^T (RC) . dZ (RC) -> fp32.  dwb: same, bf16 out.  tt: A^T (RC) . B^T (KC) -> bf16.
 #define C3_GEMM_BF16_D_KINDS(T, WM, WN, BK, ST, BT)                                  \
     C3_GEMM_BF16_D(c3_gemm_bf16_fwd_##T, WM, WN, true, false, 1, BK, ST, BT)         \
@@ -868,6 +876,7 @@ C3_GEMM_BF16_PP_KINDS(d256pp, 32, 4)
     C3_GEMM_BF16_D(c3_gemm_bf16_dw_##T, WM, WN, false, false, 2, BK, ST, BT)         \
     C3_GEMM_BF16_D(c3_gemm_bf16_dwb_##T, WM, WN, false, false, 0, BK, ST, BT)        \
     C3_GEMM_BF16_D(c3_gemm_bf16_tt_##T, WM, WN, false, true, 0, BK, ST, BT)        \
+    C3_GEMM_BF16_D(c3_gemm_bf16_fwdt_##T, WM, WN, true, true, 1, BK, ST, BT)       \
     C3_GEMM_BF16_D(c3_gemm_bf16_fwdf_##T, WM, WN, true, false, 2, BK, ST, BT)      \
     C3_GEMM_BF16_D(c3_gemm_bf16_dxf_##T, WM, WN, true, true, 2, BK, ST, BT)        \
     C3_GEMM_BF16_D(c3_gemm_bf16_ttf_##T, WM, WN, false, true, 2, BK, ST, BT)
@@ -889,6 +898,7 @@ C3_GEMM_BF16_D_KINDS(d128w4, 2, 2, 64, 2, 128)
     C3_GEMM_BF16_RQ(c3_gemm_bf16_dw_##T, false, false, 2, BK, ST)          \
     C3_GEMM_BF16_RQ(c3_gemm_bf16_dwb_##T, false, false, 0, BK, ST)         \
     C3_GEMM_BF16_RQ(c3_gemm_bf16_tt_##T, false, true, 0, BK, ST)          \
+    C3_GEMM_BF16_RQ(c3_gemm_bf16_fwdt_##T, true, true, 1, BK, ST)         \
     C3_GEMM_BF16_RQ(c3_gemm_bf16_fwdf_##T, true, false, 2, BK, ST)        \
     C3_GEMM_BF16_RQ(c3_gemm_bf16_dxf_##T, true, true, 2, BK, ST)          \
     C3_GEMM_BF16_RQ(c3_gemm_bf16_ttf_##T, false, true, 2, BK, ST)
@@ -938,5 +948,35 @@ extern "C" __global__ __launch_bounds__(256) void c3_splitk_reduce(SplitReduceAr
             ((unsigned short*)a.C)[m * a.ldc + n] = f32_to_bf16_rne(y);
         else
             ((float*)a.C)[m * a.ldc + n] = y;
+    }
+}
+
+// bf16 transpose: out[c * R + r] = in[r * C + c] for in [R, C] (row-major).
+// 64x64 tiles through LDS (rows padded to 72 elements): each thread loads two
+// 16-byte row pieces, then gathers 8 elements of one column into a 16-byte
+// store.  R and C are multiples of 8 (host-checked); edge tiles are bounded.
+extern "C" __global__ __launch_bounds__(256) void c3_transpose_bf16(const unsigned short* __restrict__ in,
+                                                                   unsigned short* __restrict__ out, int64_t R,
+                                                                   int64_t C) {
+    __shared__ __attribute__((aligned(16))) unsigned short t[64][72];
+    const int tid = threadIdx.x;
+    const int64_t tc = (int64_t)blockIdx.x * 64, tr = (int64_t)blockIdx.y * 64;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int r = tid / 8 + 32 * i, c = 8 * (tid % 8);
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (tr + r < R && tc + c < C) v = __builtin_nontemporal_load((const u32x4*)(in + (tr + r) * C + tc + c));
+        *(u32x4*)&t[r][c] = v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int c = tid / 8 + 32 * i, r = 8 * (tid % 8);  // output row c (input column), input rows r..r+7
+        if (tc + c < C && tr + r < R) {
+            u32x4 w;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) w[j] = (uint32_t)t[r + 2 * j][c] | ((uint32_t)t[r + 2 * j + 1][c] << 16);
+            *(u32x4*)(out + (tc + c) * R + tr + r) = w;
+        }
     }
 }

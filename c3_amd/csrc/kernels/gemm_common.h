@@ -67,6 +67,34 @@ __device__ __forceinline__ float act_apply(float v, int act) {
     return v;
 }
 
+// The same activations with ACT fixed at compile time.  Epilogues dispatch on
+// the runtime act once (with_act) and run an element loop compiled for that
+// activation alone: a loop calling act_apply per element carries the sigmoid
+// and tanh code at every element (tens of KiB of instructions fetched by every
+// block even for ReLU).
+template <int ACT>
+__device__ __forceinline__ float act_c(float v) {
+    if (ACT == 1) return fmaxf(v, 0.0f);
+    if (ACT == 2) return 1.0f / (1.0f + expf(-v));
+    if (ACT == 3) return tanhf(v);
+    return v;
+}
+
+template <int V>
+struct ActTag {
+    static constexpr int value = V;
+};
+
+template <class F>
+__device__ __forceinline__ void with_act(int act, F&& f) {
+    switch (act) {
+        case 1: f(ActTag<1>{}); break;
+        case 2: f(ActTag<2>{}); break;
+        case 3: f(ActTag<3>{}); break;
+        default: f(ActTag<0>{}); break;
+    }
+}
+
 __device__ __forceinline__ unsigned short f32_to_bf16_rne(float x) {
     uint32_t u = __float_as_uint(x);
     if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (unsigned short)((u >> 16) | 0x40u);

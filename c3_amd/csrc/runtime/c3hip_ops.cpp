@@ -44,11 +44,12 @@ bool ew_is_binary(int op) {
 
 // ---- GEMM planning -------------------------------------------------------
 
-enum class Kind { Fwd, Dx, DxMask, Dw, DwMask, DwB, TT };
+enum class Kind { Fwd, FwdT, Dx, DxMask, Dw, DwMask, DwB, TT };
 
 const char* kind_name(Kind k) {
     switch (k) {
         case Kind::Fwd: return "fwd";
+        case Kind::FwdT: return "fwdt";
         case Kind::Dx: return "dx";
         case Kind::DxMask: return "dx_mask";
         case Kind::Dw: return "dw";
@@ -195,7 +196,12 @@ const Tile* choose_bf16_direct(Kind kind, const GemmArgs& a, bool* unsupported, 
 // adds them in split order and applies the kind's epilogue (forward: bias and
 // activation, bf16 out; dW: fp32 out; the others: bf16 out).
 int run_split(Kind kind, const GemmArgs& a0, const Tile* d, int S, hipStream_t stream) {
-    const char* kn = kind == Kind::Fwd ? "fwdf" : kind == Kind::Dx ? "dxf" : kind == Kind::TT ? "ttf" : "dw";
+    // fp32-output kernel of the same operand layouts (FwdT: both k-contiguous, as dX).
+    const char* kn = kind == Kind::Fwd                          ? "fwdf"
+                     : (kind == Kind::Dx || kind == Kind::FwdT) ? "dxf"
+                     : kind == Kind::TT                         ? "ttf"
+                                                                : "dw";
+    const bool fwd = kind == Kind::Fwd || kind == Kind::FwdT;
     float* ws = nullptr;
     const int64_t slice = a0.M * a0.N;
     hipError_t e = hipMallocAsync((void**)&ws, (size_t)S * (size_t)slice * sizeof(float), stream);
@@ -216,13 +222,13 @@ int run_split(Kind kind, const GemmArgs& a0, const Tile* d, int S, hipStream_t s
         SplitReduceArgs r{};
         r.ws = ws;
         r.C = a0.C;
-        r.bias = kind == Kind::Fwd ? a0.bias : nullptr;
+        r.bias = fwd ? a0.bias : nullptr;
         r.M = a0.M;
         r.N = a0.N;
         r.ldc = a0.ldc;
         r.slice = slice;
         r.S = S;
-        r.act = kind == Kind::Fwd ? a0.act : 0;
+        r.act = fwd ? a0.act : 0;
         r.out_bf16 = kind == Kind::Dw ? 0 : 1;
         const int64_t threads = a0.M * ((a0.N + 3) / 4);
         void* rargs[] = {&r};
@@ -264,6 +270,7 @@ int run_gemm(int dtype, Kind kind, const GemmArgs& a0, bool a_kc, bool b_kc, hip
                                                         " cannot run this GEMM (masked operand, db side output, "
                                                         "K not a multiple of its k depth, or M or N below 8)");
         if (d && split > 1) return run_split(kind, a, d, split, stream);
+        if (!d && kind == Kind::FwdT) return set_error(C3HIP_ERR_UNSUPPORTED, "transposed-W forward needs a direct tile");
         if (d) {
             char name[96];
             std::snprintf(name, sizeof(name), "c3_gemm_bf16_%s_%s", kind_name(kind), d->name);
@@ -287,6 +294,44 @@ int run_gemm(int dtype, Kind kind, const GemmArgs& a0, bool a_kc, bool b_kc, hip
     if (blocks > 0x7fffffff) return set_error(C3HIP_ERR_TOO_LARGE, "GEMM grid too large");
     void* args[] = {&a};
     return launch(name, dim3((unsigned)blocks), dim3(t->threads), args, stream);
+}
+
+// bf16 forward with W transposed first: both GEMM operands are then
+// k-contiguous and read with ds_read_b128 instead of transposed LDS reads.
+// Same tile, split and k order as the plain forward, so the same bits.
+// Opt-in (C3_HIP_BF16_WT=1, whenever a direct tile runs the forward): measured
+// on MI355X with the transpose included it gains 4% at 8192x4096x4096 and
+// loses 1.5% at 16384x4096x8192 and 27% at 4096x1024x4096, so the size
+// heuristic never picks it.
+bool bf16_fwd_transposed(const GemmArgs& a) {
+    const char* env = std::getenv("C3_HIP_BF16_WT");
+    if (!env || env[0] != '1') return false;
+    if (a.K % 8 != 0 || a.N % 8 != 0 || !aligned16(a.A) || !aligned16(a.B)) return false;
+    if ((a.K + 63) / 64 > 65535 || (a.N + 63) / 64 > 0x7fffffff) return false;  // transpose grid
+    bool unsupported = false;
+    int split = 1;
+    return choose_bf16_direct(Kind::Fwd, a, &unsupported, &split) != nullptr;
+}
+
+int linear_fwd_wt(const GemmArgs& a0, hipStream_t stream) {
+    void* wt = nullptr;
+    hipError_t e = hipMallocAsync(&wt, (size_t)(a0.K * a0.N) * 2, stream);
+    if (e != hipSuccess) return set_error(C3HIP_ERR_HIP, std::string("hipMallocAsync(W^T): ") + hipGetErrorString(e));
+    const void* w = a0.B;
+    int64_t R = a0.K, Cc = a0.N;
+    void* targs[] = {(void*)&w, &wt, &R, &Cc};
+    int rc = launch("c3_transpose_bf16", dim3((unsigned)((Cc + 63) / 64), (unsigned)((R + 63) / 64)), dim3(256), targs,
+                    stream);
+    if (rc == C3HIP_OK) {
+        GemmArgs a = a0;
+        a.B = wt;
+        a.ldb = a0.K;
+        rc = run_gemm(C3HIP_BF16, Kind::FwdT, a, true, true, stream);
+    }
+    e = hipFreeAsync(wt, stream);
+    if (rc == C3HIP_OK && e != hipSuccess)
+        rc = set_error(C3HIP_ERR_HIP, std::string("hipFreeAsync(W^T): ") + hipGetErrorString(e));
+    return rc;
 }
 
 int check_elems(const char* what, int64_t rows, int64_t cols) {
@@ -585,6 +630,7 @@ int c3hip_linear_fwd(int dtype, const void* X, const void* W, const float* b, vo
     a.M = M; a.N = N; a.K = K;
     a.lda = K; a.ldb = N; a.ldc = N;
     a.act = act;
+    if (dtype == C3HIP_BF16 && M > 0 && N > 0 && K > 0 && bf16_fwd_transposed(a)) return linear_fwd_wt(a, (hipStream_t)stream);
     return run_gemm(dtype, Kind::Fwd, a, true, false, (hipStream_t)stream);
 }
 

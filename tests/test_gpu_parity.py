@@ -473,3 +473,33 @@ def test_bf16_split_k_real_values(gpu, stream):
     bound = gemm_bound(X, W, K)
     assert_close_gemm(gY, rY, bound, BF16_TOL, out_round=2.0 ** -8, what="Y bf16 split")
     mask_flips(gY, z, bound + 2.0 ** -8 * np.abs(z))
+
+
+# Transposed-W forward (bf16, opt-in with C3_HIP_BF16_WT=1): W is transposed
+# into a workspace and the GEMM reads both operands k-contiguous.  Same tile,
+# split and k order as the plain forward, so the same bits: integer inputs
+# against the exact product, real inputs against the plain path bit for bit.
+# Shapes: a 256x256-tile forward, a split-K forward, a 128x128-tile forward.
+@pytest.mark.parametrize("M,K,Nn", [(4096, 256, 264), (576, 8192, 576), (1000, 512, 1024)])
+def test_bf16_fwd_transposed_w(gpu, stream, monkeypatch, M, K, Nn):
+    from tests.parity import dev_bf16
+
+    X, W, b = ints(121, (M, K)), ints(122, (K, Nn)), ints(123, Nn)
+    want = _bf16_round(np.maximum(X.astype(np.float64) @ W.astype(np.float64) + b, 0.0).astype(np.float32))
+    Xr = _bf16_round(O.normal(124, (M, K)))
+    Wr = _bf16_round(O.normal(125, (K, Nn), 0.0, 1.0 / np.sqrt(K)))
+    br = O.normal(126, Nn, 0.0, 0.1)
+    outs = {}
+    for mode in ("1", "0", None):
+        if mode is None:
+            monkeypatch.delenv("C3_HIP_BF16_WT", raising=False)
+        else:
+            monkeypatch.setenv("C3_HIP_BF16_WT", mode)
+        Y = empty((M, Nn), dtype=torch.bfloat16)
+        N.linear_fwd(N.BF16, ptr(dev_bf16(X)), ptr(dev_bf16(W)), ptr(dev(b)), ptr(Y), M, K, Nn, 1, stream)
+        same_bits(host(Y), want)
+        Yr = empty((M, Nn), dtype=torch.bfloat16)
+        N.linear_fwd(N.BF16, ptr(dev_bf16(Xr)), ptr(dev_bf16(Wr)), ptr(dev(br)), ptr(Yr), M, K, Nn, 1, stream)
+        outs[mode] = host(Yr)
+    same_bits(outs["1"], outs["0"])
+    same_bits(outs[None], outs["0"])
