@@ -167,31 +167,57 @@ extern "C" __global__ __launch_bounds__(kThreads) void c3_dz_colsum_bf16(
     const int64_t r0 = chunk * rows_per_chunk;
     const int64_t r1 = min(M, r0 + rows_per_chunk);
     float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    // dZ of one 16-byte vector from its Y and dY vectors.
+    auto grad = [&](u32x4 y, u32x4 d) {
+        if (act == 1) return mask_mul8(y, d);
+        if (act == 2 || act == 3) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float lo = act_grad(bf16_to_f32((unsigned short)(y[e] & 0xffff)),
+                                          bf16_to_f32((unsigned short)(d[e] & 0xffff)), act);
+                const float hi = act_grad(bf16_to_f32((unsigned short)(y[e] >> 16)),
+                                          bf16_to_f32((unsigned short)(d[e] >> 16)), act);
+                d[e] = (uint32_t)f32_to_bf16_rne(lo) | ((uint32_t)f32_to_bf16_rne(hi) << 16);
+            }
+        }
+        return d;
+    };
+    auto sum = [&](u32x4 d) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            s[2 * e] += __uint_as_float(d[e] << 16);
+            s[2 * e + 1] += __uint_as_float(d[e] & 0xffff0000u);
+        }
+    };
     if (active) {
-        for (int64_t i = r0 + rl; i < r1; i += rb) {
+        // Four rows per iteration: their eight loads are issued before the
+        // first use (a thread walks 4..64 rows; one row at a time leaves the
+        // stream latency-bound).  Rows are still summed in row order.
+        const bool need_y = act != 0;
+        int64_t i = r0 + rl;
+        for (; i + 3 * rb < r1; i += 4 * rb) {
+            u32x4 d[4], y[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int64_t off = (i + q * rb) * N + 8 * v;
+                d[q] = __builtin_nontemporal_load((const u32x4*)(dY + off));
+                y[q] = need_y ? __builtin_nontemporal_load((const u32x4*)(Y + off)) : u32x4{0u, 0u, 0u, 0u};
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int64_t off = (i + q * rb) * N + 8 * v;
+                const u32x4 g = grad(y[q], d[q]);
+                if (dZ) *(u32x4*)(dZ + off) = g;
+                if (part) sum(g);
+            }
+        }
+        for (; i < r1; i += rb) {
             const int64_t off = i * N + 8 * v;
-            u32x4 d = __builtin_nontemporal_load((const u32x4*)(dY + off));
-            if (act == 1) {
-                d = mask_mul8(__builtin_nontemporal_load((const u32x4*)(Y + off)), d);
-            } else if (act == 2 || act == 3) {
-                const u32x4 y = __builtin_nontemporal_load((const u32x4*)(Y + off));
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float lo = act_grad(bf16_to_f32((unsigned short)(y[e] & 0xffff)),
-                                              bf16_to_f32((unsigned short)(d[e] & 0xffff)), act);
-                    const float hi = act_grad(bf16_to_f32((unsigned short)(y[e] >> 16)),
-                                              bf16_to_f32((unsigned short)(d[e] >> 16)), act);
-                    d[e] = (uint32_t)f32_to_bf16_rne(lo) | ((uint32_t)f32_to_bf16_rne(hi) << 16);
-                }
-            }
-            if (dZ) *(u32x4*)(dZ + off) = d;
-            if (part) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    s[2 * e] += __uint_as_float(d[e] << 16);
-                    s[2 * e + 1] += __uint_as_float(d[e] & 0xffff0000u);
-                }
-            }
+            const u32x4 d = __builtin_nontemporal_load((const u32x4*)(dY + off));
+            const u32x4 y = need_y ? __builtin_nontemporal_load((const u32x4*)(Y + off)) : u32x4{0u, 0u, 0u, 0u};
+            const u32x4 g = grad(y, d);
+            if (dZ) *(u32x4*)(dZ + off) = g;
+            if (part) sum(g);
         }
     }
     if (part) {
