@@ -30,13 +30,17 @@ constexpr int kPad = 4;   // floats of padding per k-row of a row-contiguous til
 
 // LDS tile layouts.  KC (k contiguous in global): [ROWS][16 k], 64 B per row,
 // the 16-byte chunk holding k 4c..4c+3 of row r stored in slot
-// c ^ ((r >> 1) & 3), so the 16-byte fragment reads of 8 consecutive rows
-// touch 8 distinct bank groups.  !KC: [16 k][ROWS + 4].
+// c ^ ((r >> 2) & 3).  A 64-byte row puts row r on bank group 4 (r & 3) +
+// slot (16-byte groups, 64 banks); a ds_read_b128 serves 16 lanes = 16
+// consecutive rows at a time, and (r & 3, (r >> 2) & 3) takes all 16 values
+// over them, so the fragment reads are conflict-free (the key (r >> 1) & 3
+// shares bit 1 with r & 3 and left a 2-way conflict); the 4-row stores stay
+// conflict-free.  !KC: [16 k][ROWS + 4].
 template <int ROWS, bool KC>
 struct Lds {
     static constexpr int STRIDE = KC ? kBK : (ROWS + kPad);
     static constexpr int SIZE = KC ? ROWS * STRIDE : kBK * STRIDE;
-    __device__ __forceinline__ static int kc_slot(int row, int chunk) { return chunk ^ ((row >> 1) & 3); }
+    __device__ __forceinline__ static int kc_slot(int row, int chunk) { return chunk ^ ((row >> 2) & 3); }
 };
 
 // Global -> register staging of one operand tile (ROWS x kBK logical, ROWS =
