@@ -177,6 +177,11 @@ float MlpTrainer::step(const Tensor& X, const void* labels, float lr, bool want_
         kept_db_.clear();
     }
     auto& B = C3BackwardCapture::getInstance();
+    // Gradients of every layer; the SGD step runs once after the backward,
+    // one launch for the weights and one for the biases (every dA is formed
+    // from the old weights either way, so the result is the same as updating
+    // each layer as soon as its gradients exist).
+    std::vector<Tensor> dWs(L), dbs(L);
     for (size_t i = L; i-- > 0;) {
         const bool relu = i + 1 < L;
         const Tensor& A = acts_[i];
@@ -205,11 +210,27 @@ float MlpTrainer::step(const Tensor& X, const void* labels, float lr, bool want_
             kept_dW_[i] = dW;
             kept_db_[i] = db;
         }
-        // dA was computed from the old W, so the update may follow at once.
-        check(c3hip_sgd_update(hipDtype(dt_), W_[i].data(), dW.data_ptr<float>(), lr, (int64_t)W_[i].numel(), st),
-              "sgd W");
-        check(c3hip_sgd_update(C3HIP_F32, b_[i].data(), db.data_ptr<float>(), lr, (int64_t)b_[i].numel(), st), "sgd b");
+        dWs[i] = dW;
+        dbs[i] = db;
         g = dA;
+    }
+    for (size_t i0 = 0; i0 < L; i0 += C3HIP_SGD_MAX_TENSORS) {
+        const size_t k = std::min<size_t>(C3HIP_SGD_MAX_TENSORS, L - i0);
+        void* w[C3HIP_SGD_MAX_TENSORS];
+        void* bb[C3HIP_SGD_MAX_TENSORS];
+        const float* gw[C3HIP_SGD_MAX_TENSORS];
+        const float* gb[C3HIP_SGD_MAX_TENSORS];
+        int64_t nw[C3HIP_SGD_MAX_TENSORS], nb[C3HIP_SGD_MAX_TENSORS];
+        for (size_t t = 0; t < k; ++t) {
+            w[t] = W_[i0 + t].data();
+            gw[t] = dWs[i0 + t].data_ptr<float>();
+            nw[t] = (int64_t)W_[i0 + t].numel();
+            bb[t] = b_[i0 + t].data();
+            gb[t] = dbs[i0 + t].data_ptr<float>();
+            nb[t] = (int64_t)b_[i0 + t].numel();
+        }
+        check(c3hip_sgd_update_multi(hipDtype(dt_), (int)k, w, gw, nw, lr, st), "sgd W");
+        check(c3hip_sgd_update_multi(C3HIP_F32, (int)k, bb, gb, nb, lr, st), "sgd b");
     }
     stats_.steps++;
     // Every ReLU layer as a region (MatMul+Add alone is below the cost

@@ -279,15 +279,36 @@ __device__ __forceinline__ void gemm_f32_body(const GemmArgs& p) {
 
 }  // namespace
 
+namespace {
+// Split-K: block row blockIdx.y multiplies k in [y * split_k, y * split_k +
+// split_k) (the masks follow their operands) and writes the raw partial
+// product to C + y * c_split; the host passes no bias, activation or db, and
+// c3_splitk_reduce adds the partials and applies the epilogue.
+template <bool AK, bool BKC>
+__device__ __forceinline__ GemmArgs split_args_f32(const GemmArgs& p) {
+    if (p.split_k == 0) return p;
+    GemmArgs q = p;
+    const int64_t k0 = (int64_t)blockIdx.y * p.split_k;
+    const int64_t ao = AK ? k0 : k0 * p.lda, bo = BKC ? k0 : k0 * p.ldb;
+    q.A = (const float*)p.A + ao;
+    if (p.Amask) q.Amask = (const float*)p.Amask + ao;
+    q.B = (const float*)p.B + bo;
+    if (p.Bmask) q.Bmask = (const float*)p.Bmask + bo;
+    q.K = min(p.split_k, p.K - k0);
+    q.C = (float*)p.C + (int64_t)blockIdx.y * p.c_split;
+    return q;
+}
+}  // namespace
+
 // One extern "C" symbol per (layout, fusion, tile, vector) case.
 // Tile suffix _tBMxBN_wWMxWN; _v: vectorised operand loads (contiguous extent
 // % 4 == 0 and 16-byte aligned bases), _s: scalar loads.
 #define C3_GEMM_F32_ONE(NAME, BM, BN, WM, WN, OCC, AK, BKC, AMASK, BMASK, DB)                         \
     extern "C" __global__ __launch_bounds__(64 * WM * WN, OCC) void NAME##_v(GemmArgs p) {           \
-        gemm_f32_body<BM, BN, WM, WN, AK, BKC, AMASK, BMASK, DB, true>(p);                           \
+        gemm_f32_body<BM, BN, WM, WN, AK, BKC, AMASK, BMASK, DB, true>(split_args_f32<AK, BKC>(p));  \
     }                                                                                               \
     extern "C" __global__ __launch_bounds__(64 * WM * WN, OCC) void NAME##_s(GemmArgs p) {           \
-        gemm_f32_body<BM, BN, WM, WN, AK, BKC, AMASK, BMASK, DB, false>(p);                          \
+        gemm_f32_body<BM, BN, WM, WN, AK, BKC, AMASK, BMASK, DB, false>(split_args_f32<AK, BKC>(p)); \
     }
 
 // Kinds: fwd (A=X k-contig, B=W [K,N]); dx/dx_mask (A=dY[, masked by Y], B=W as [N][K]);

@@ -122,9 +122,10 @@ extern "C" __global__ __launch_bounds__(kThreads) void c3_cast_bf16_f32(const un
 // the same on any IEEE machine.  bf16 parameters are widened, updated in
 // fp32 and rounded back to nearest-even.
 template <bool BF16>
-__device__ __forceinline__ void sgd_body(void* __restrict__ w, const float* __restrict__ g, float lr, int64_t n) {
+__device__ __forceinline__ void sgd_body(void* __restrict__ w, const float* __restrict__ g, float lr, int64_t n,
+                                         int64_t block) {
 #pragma clang fp contract(off)
-    const int64_t i0 = ((int64_t)blockIdx.x * kThreads + threadIdx.x) * 4;
+    const int64_t i0 = (block * kThreads + threadIdx.x) * 4;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const int64_t i = i0 + e;
@@ -142,9 +143,32 @@ __device__ __forceinline__ void sgd_body(void* __restrict__ w, const float* __re
 }
 
 extern "C" __global__ __launch_bounds__(kThreads) void c3_sgd_f32(void* w, const float* g, float lr, int64_t n) {
-    sgd_body<false>(w, g, lr, n);
+    sgd_body<false>(w, g, lr, n, blockIdx.x);
 }
 
 extern "C" __global__ __launch_bounds__(kThreads) void c3_sgd_bf16(void* w, const float* g, float lr, int64_t n) {
-    sgd_body<true>(w, g, lr, n);
+    sgd_body<true>(w, g, lr, n, blockIdx.x);
 }
+
+// The same step on up to kSgdMaxTensors parameters in one launch: tensor t
+// owns blocks first[t] .. first[t + 1] - 1 (a uniform scan per block).
+constexpr int kSgdMaxTensors = 16;
+struct SgdMultiArgs {
+    void* w[kSgdMaxTensors];
+    const float* g[kSgdMaxTensors];
+    int64_t n[kSgdMaxTensors];
+    int64_t first[kSgdMaxTensors + 1];
+    int count;
+    float lr;
+};
+
+template <bool BF16>
+__device__ __forceinline__ void sgd_multi_body(const SgdMultiArgs& a) {
+    const int64_t b = blockIdx.x;
+    int t = 0;
+    while (t + 1 < a.count && b >= a.first[t + 1]) ++t;
+    sgd_body<BF16>(a.w[t], a.g[t], a.lr, a.n[t], b - a.first[t]);
+}
+
+extern "C" __global__ __launch_bounds__(kThreads) void c3_sgd_multi_f32(SgdMultiArgs a) { sgd_multi_body<false>(a); }
+extern "C" __global__ __launch_bounds__(kThreads) void c3_sgd_multi_bf16(SgdMultiArgs a) { sgd_multi_body<true>(a); }

@@ -1,6 +1,8 @@
 // c3hip_internal.h -- shared helpers of the C-ABI implementation files.
 #pragma once
 #include <hip/hip_runtime.h>
+
+#include "c3hip.h"
 #include <stdint.h>
 
 #include <string>
@@ -40,6 +42,17 @@ struct GemmArgs {
     int _pad;
     int64_t split_k;
     int64_t c_split;
+};
+
+// Argument block of c3_sgd_multi_* (mirrors SgdMultiArgs in
+// c3_amd/csrc/kernels/loss.hip).
+struct SgdMultiArgs {
+    void* w[C3HIP_SGD_MAX_TENSORS];
+    const float* g[C3HIP_SGD_MAX_TENSORS];
+    int64_t n[C3HIP_SGD_MAX_TENSORS];
+    int64_t first[C3HIP_SGD_MAX_TENSORS + 1];
+    int count;
+    float lr;
 };
 
 // Argument block of c3_splitk_reduce (mirrors SplitReduceArgs in

@@ -78,4 +78,36 @@ int c3hip_sgd_update(int dtype, void* w, const float* g, float lr, int64_t n, vo
                   (hipStream_t)stream);
 }
 
+int c3hip_sgd_update_multi(int dtype, int count, void* const* w, const float* const* g, const int64_t* n, float lr,
+                           void* stream) {
+    clear_error();
+    if (dtype != C3HIP_F32 && dtype != C3HIP_BF16) return set_error(C3HIP_ERR_INVALID, "unknown dtype");
+    if (count < 0 || count > C3HIP_SGD_MAX_TENSORS)
+        return set_error(C3HIP_ERR_INVALID, "count must be in 0.." + std::to_string(C3HIP_SGD_MAX_TENSORS));
+    if (count == 0) return C3HIP_OK;
+    if (!w || !g || !n) return set_error(C3HIP_ERR_INVALID, "null array");
+    SgdMultiArgs a{};
+    int64_t blocks = 0;
+    int k = 0;
+    for (int t = 0; t < count; ++t) {
+        if (n[t] < 0) return set_error(C3HIP_ERR_INVALID, "n < 0");
+        if (n[t] == 0) continue;
+        if (!w[t] || !g[t]) return set_error(C3HIP_ERR_INVALID, "null pointer");
+        a.w[k] = w[t];
+        a.g[k] = g[t];
+        a.n[k] = n[t];
+        a.first[k] = blocks;
+        blocks += (n[t] + 4 * kThreads - 1) / (4 * kThreads);
+        ++k;
+    }
+    if (k == 0) return C3HIP_OK;
+    if (blocks > 0x7fffffff) return set_error(C3HIP_ERR_TOO_LARGE, "sgd grid too large");
+    a.first[k] = blocks;
+    a.count = k;
+    a.lr = lr;
+    void* args[] = {&a};
+    return launch(dtype == C3HIP_BF16 ? "c3_sgd_multi_bf16" : "c3_sgd_multi_f32", dim3((unsigned)blocks),
+                  dim3(kThreads), args, (hipStream_t)stream);
+}
+
 }  // extern "C"

@@ -255,6 +255,61 @@ bool vec_ok(bool kc, int64_t rows, int64_t k, int64_t ld, const void* p, const v
     return aligned16(p) && aligned16(pm);
 }
 
+// fp32 split-K for a small grid over a long k range (a train step's first
+// layer at batch 128: 8 tiles of 64x64 over K = 784): the 64x64 kernel on
+// fewer than 32 tiles with K >= 512 and no db side output splits k into
+// 16-aligned parts at least 128 deep, up to 256 blocks; 0 = no split.  A
+// forced tile never splits.
+int plan_split_f32(const GemmArgs& a, const Tile* t) {
+    if (!t_tile_f32.empty() || std::getenv("C3_HIP_GEMM_TILE")) return 0;
+    if (t->bm != 64 || a.db != nullptr || a.K < 512) return 0;
+    const int64_t tiles = tile_count(a, t);
+    if (tiles >= 32) return 0;
+    int64_t S = std::min<int64_t>(256 / tiles, a.K / 128);
+    if ((double)S * (double)a.M * (double)a.N * 4.0 > (double)(256u << 20)) S = (256 << 20) / (a.M * a.N * 4);
+    return S >= 2 ? (int)S : 0;
+}
+
+int run_split_f32(Kind kind, const GemmArgs& a0, const Tile* t, int S, bool vec, hipStream_t stream) {
+    const int64_t split_k = ((a0.K + S - 1) / S + 15) / 16 * 16;
+    S = (int)((a0.K + split_k - 1) / split_k);
+    const int64_t slice = a0.M * a0.N;
+    float* ws = nullptr;
+    hipError_t e = hipMallocAsync((void**)&ws, (size_t)S * (size_t)slice * sizeof(float), stream);
+    if (e != hipSuccess) return set_error(C3HIP_ERR_HIP, std::string("hipMallocAsync(split-K): ") + hipGetErrorString(e));
+    GemmArgs g = a0;
+    g.C = ws;
+    g.ldc = a0.N;
+    g.bias = nullptr;
+    g.act = 0;
+    g.split_k = split_k;
+    g.c_split = slice;
+    char name[96];
+    std::snprintf(name, sizeof(name), "c3_gemm_f32_%s_%s_%s", kind_name(kind), t->name, vec ? "v" : "s");
+    void* args[] = {&g};
+    int rc = launch(name, dim3((unsigned)tile_count(a0, t), (unsigned)S), dim3(t->threads), args, stream);
+    if (rc == C3HIP_OK) {
+        SplitReduceArgs r{};
+        r.ws = ws;
+        r.C = a0.C;
+        r.bias = a0.bias;
+        r.M = a0.M;
+        r.N = a0.N;
+        r.ldc = a0.ldc;
+        r.slice = slice;
+        r.S = S;
+        r.act = a0.act;
+        r.out_bf16 = 0;
+        const int64_t threads = a0.M * ((a0.N + 3) / 4);
+        void* rargs[] = {&r};
+        rc = launch("c3_splitk_reduce", dim3((unsigned)((threads + 255) / 256)), dim3(256), rargs, stream);
+    }
+    e = hipFreeAsync(ws, stream);
+    if (rc == C3HIP_OK && e != hipSuccess)
+        rc = set_error(C3HIP_ERR_HIP, std::string("hipFreeAsync(split-K): ") + hipGetErrorString(e));
+    return rc;
+}
+
 int run_gemm(int dtype, Kind kind, const GemmArgs& a0, bool a_kc, bool b_kc, hipStream_t stream) {
     GemmArgs a = a0;
     if (a.M == 0 || a.N == 0) return C3HIP_OK;
@@ -288,6 +343,7 @@ int run_gemm(int dtype, Kind kind, const GemmArgs& a0, bool a_kc, bool b_kc, hip
     }
     const Tile* t = choose_f32_tile(kind, a.M, a.N);
     const bool vec = vec_ok(a_kc, a.M, a.K, a.lda, a.A, a.Amask) && vec_ok(b_kc, a.N, a.K, a.ldb, a.B, a.Bmask);
+    if (const int S = plan_split_f32(a, t)) return run_split_f32(kind, a, t, S, vec, stream);
     char name[96];
     std::snprintf(name, sizeof(name), "c3_gemm_f32_%s_%s_%s", kind_name(kind), t->name, vec ? "v" : "s");
     const int64_t blocks = ((a.M + t->bm - 1) / t->bm) * ((a.N + t->bn - 1) / t->bn);

@@ -57,6 +57,8 @@ SIGNATURES = {
     "c3hip_softmax_ce": (_int, [_int, _vp, _vp, _vp, _vp, _i64, _i64, _vp]),
     "c3hip_cast": (_int, [_int, _int, _vp, _vp, _i64, _vp]),
     "c3hip_sgd_update": (_int, [_int, _vp, _vp, _f, _i64, _vp]),
+    "c3hip_sgd_update_multi": (_int, [_int, _int, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_void_p),
+                                      ctypes.POINTER(ctypes.c_int64), _f, _vp]),
 }
 
 
@@ -172,3 +174,15 @@ def cast(src_dtype: int, dst_dtype: int, inp: int, out: int, n: int, stream: int
 
 def sgd_update(dtype: int, w: int, g: int, lr: float, n: int, stream: int = 0) -> None:
     _check("c3hip_sgd_update", load().c3hip_sgd_update(dtype, w, g, lr, n, stream))
+
+
+SGD_MAX_TENSORS = 16
+
+
+def sgd_update_multi(dtype: int, ws, gs, ns, lr: float, stream: int = 0) -> None:
+    """c3hip_sgd_update on several parameters of one dtype in one launch."""
+    k = len(ws)
+    W = (ctypes.c_void_p * max(k, 1))(*ws)
+    G = (ctypes.c_void_p * max(k, 1))(*gs)
+    Nn = (ctypes.c_int64 * max(k, 1))(*ns)
+    _check("c3hip_sgd_update_multi", load().c3hip_sgd_update_multi(dtype, k, W, G, Nn, lr, stream))

@@ -261,6 +261,20 @@ int c3hip_cast(int src_dtype, int dst_dtype, const void* in, void* out, int64_t 
  */
 int c3hip_sgd_update(int dtype, void* w, const float* g, float lr, int64_t n, void* stream);
 
+/* Most tensors c3hip_sgd_update_multi takes in one call. */
+#define C3HIP_SGD_MAX_TENSORS 16
+
+/*
+ * c3hip_sgd_update on `count` parameters of one dtype (w[t], g[t], n[t]) in a
+ * single launch, each element updated exactly as c3hip_sgd_update does (the
+ * same bits).  count <= C3HIP_SGD_MAX_TENSORS; w, g and n are host arrays of
+ * device pointers and sizes.  No reference counterpart (the optimizer belongs
+ * to the host framework); it replaces one launch per weight and bias in a
+ * train step.
+ */
+int c3hip_sgd_update_multi(int dtype, int count, void* const* w, const float* const* g, const int64_t* n, float lr,
+                           void* stream);
+
 #ifdef __cplusplus
 }
 #endif

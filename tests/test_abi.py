@@ -61,7 +61,7 @@ def test_code_objects_hold_every_dispatched_kernel():
     assert {"c3_colsum_partial_f32", "c3_colsum_final_f32", "c3_rowsum_f32"} <= red
     loss = _kernel_symbols(LIB / "loss.hsaco")
     assert {"c3_softmax_ce_f32", "c3_softmax_ce_bf16", "c3_cast_f32_bf16", "c3_cast_bf16_f32", "c3_sgd_f32",
-            "c3_sgd_bf16"} <= loss
+            "c3_sgd_bf16", "c3_sgd_multi_f32", "c3_sgd_multi_bf16"} <= loss
 
 
 # Argument validation runs before any HIP call, so it is testable on the CPU.
@@ -156,6 +156,19 @@ def test_train_step_helper_validation():
     assert _rc("c3hip_cast", 0, 1, None, None, 0, None) == native.OK
     assert _rc("c3hip_sgd_update", 0, None, 16, 0.1, 4, None) == native.ERR_INVALID
     assert _rc("c3hip_sgd_update", 0, 16, 16, 0.1, -1, None) == native.ERR_INVALID
+    import ctypes
+
+    P = ctypes.c_void_p * 2
+    I = ctypes.c_int64 * 2
+    f = ctypes.c_float(0.1)
+    assert _rc("c3hip_sgd_update_multi", 0, 17, P(16, 16), P(16, 16), I(4, 4), f, None) == native.ERR_INVALID
+    assert _rc("c3hip_sgd_update_multi", 0, -1, P(16, 16), P(16, 16), I(4, 4), f, None) == native.ERR_INVALID
+    assert _rc("c3hip_sgd_update_multi", 2, 2, P(16, 16), P(16, 16), I(4, 4), f, None) == native.ERR_INVALID
+    assert _rc("c3hip_sgd_update_multi", 0, 2, None, P(16, 16), I(4, 4), f, None) == native.ERR_INVALID
+    assert _rc("c3hip_sgd_update_multi", 0, 2, P(16, None), P(16, 16), I(4, 4), f, None) == native.ERR_INVALID
+    assert _rc("c3hip_sgd_update_multi", 0, 2, P(16, 16), P(16, 16), I(4, -1), f, None) == native.ERR_INVALID
+    assert _rc("c3hip_sgd_update_multi", 0, 0, None, None, None, f, None) == native.OK  # nothing to do
+    assert _rc("c3hip_sgd_update_multi", 0, 2, P(None, None), P(None, None), I(0, 0), f, None) == native.OK
 
 
 def test_python_binding_raises_with_message():

@@ -503,3 +503,48 @@ def test_bf16_fwd_transposed_w(gpu, stream, monkeypatch, M, K, Nn):
         outs[mode] = host(Yr)
     same_bits(outs["1"], outs["0"])
     same_bits(outs[None], outs["0"])
+
+
+# fp32 split-K: the 64x64 kernel on fewer than 32 tiles over K >= 512 runs as
+# 16-aligned k splits whose fp32 partials c3_splitk_reduce adds (with the bias
+# and activation).  (128, 784, 256): the forward splits (a train step's first
+# layer); (128, 256, 784): the masked dX splits (k = N = 784) while dW keeps
+# its db side output and does not.
+@pytest.mark.parametrize("M,K,Nn", [(128, 784, 256), (128, 256, 784), (70, 1000, 90)])
+def test_f32_split_k_bit_exact(gpu, stream, M, K, Nn):
+    X, W, b = ints(131, (M, K)), ints(132, (K, Nn)), ints(133, Nn)
+    Y = empty((M, Nn))
+    N.linear_fwd(N.F32, ptr(dev(X)), ptr(dev(W)), ptr(dev(b)), ptr(Y), M, K, Nn, 1, stream)
+    rY = O.linear_fwd(X, W, b, 1)
+    same_bits(host(Y), rY)
+    dY = ints(134, (M, Nn))
+    gX, gW, gb = _run_bwd(stream, X, W, rY, dY, 1)
+    rX, rW, rb = O.linear_bwd(X, W, rY, dY, 1)
+    same_bits(gX, rX)
+    same_bits(gW, rW)
+    same_bits(gb, rb)
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_f32_split_k_matmul_transposes(gpu, stream, ta, tb):
+    M, K, Nn = 96, 1000, 80
+    A = ints(141, (K, M) if ta else (M, K))
+    B = ints(142, (Nn, K) if tb else (K, Nn))
+    C = empty((M, Nn))
+    N.matmul(N.F32, ptr(dev(A)), ptr(dev(B)), ptr(C), M, K, Nn, bool(ta), bool(tb), stream)
+    same_bits(host(C), O.matmul(A, B, transA=bool(ta), transB=bool(tb)))
+
+
+@pytest.mark.parametrize("act", [1, 2])
+def test_f32_split_k_real(gpu, stream, act):
+    M, K, Nn = 128, 784, 256
+    X = O.normal(151, (M, K))
+    W = O.normal(152, (K, Nn), 0.0, 1.0 / np.sqrt(K))
+    b = O.normal(153, Nn, 0.0, 0.1)
+    Y = empty((M, Nn))
+    N.linear_fwd(N.F32, ptr(dev(X)), ptr(dev(W)), ptr(dev(b)), ptr(Y), M, K, Nn, act, stream)
+    t = O.matmul(X, W)
+    ref = O.bias_act(t, b, act)
+    # ReLU: the GEMM bound; sigmoid is 1/4-Lipschitz and adds a few ulp.
+    bound = gemm_bound(X, W, K) + (8.0 * 2.0 ** -24 if act == 2 else 0.0)
+    assert_close_gemm(host(Y), ref, bound, FP32_TOL, out_round=(4.0 * 2.0 ** -24 if act == 2 else 0.0), what="Y split")

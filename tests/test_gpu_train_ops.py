@@ -136,3 +136,26 @@ def test_sgd_update(gpu, stream, n):
     nan = np.isnan(O.bf16_bits_to_f32(ref))
     assert np.array_equal(np.isnan(O.bf16_bits_to_f32(got)), nan)
     assert np.array_equal(got[~nan], ref[~nan])
+
+
+def test_sgd_update_multi(gpu, stream):
+    # Several parameters of assorted sizes (a zero-length one, odd tails,
+    # 16 = the most one call takes) in one launch: every element as the
+    # single-tensor update computes it (the oracle's), fp32 and bf16.
+    sizes = [1, 0, 1027, 4096, 7, 256 * 1024 + 5, 3, 64, 65, 1, 2, 5000, 9, 10, 11, 12345]
+    assert len(sizes) == N.SGD_MAX_TENSORS
+    lr = 0.031
+    ws = [O.normal(560 + i, n) for i, n in enumerate(sizes)]
+    gs = [O.normal(580 + i, n) for i, n in enumerate(sizes)]
+    dws = [dev(w) for w in ws]
+    dgs = [dev(g) for g in gs]
+    N.sgd_update_multi(N.F32, [ptr(t) for t in dws], [ptr(t) for t in dgs], sizes, lr, stream)
+    for w, g, t in zip(ws, gs, dws):
+        same_bits(host(t), O.sgd_update(w, g, lr))
+    wbs = [O.pack_bf16(w) for w in ws]
+    tbs = [torch.from_numpy(wb.view(np.int16).copy()).to("cuda:0") for wb in wbs]
+    N.sgd_update_multi(N.BF16, [ptr(t) for t in tbs], [ptr(t) for t in dgs], sizes, lr, stream)
+    torch.cuda.synchronize()
+    for wb, g, t in zip(wbs, gs, tbs):
+        got = t.cpu().numpy().view(np.uint16)
+        assert np.array_equal(got, O.sgd_update(wb, g, lr))
