@@ -492,22 +492,34 @@ __device__ __forceinline__ void store_block_t(const GemmArgs& p, const f32x16& a
 
 // Blocks are visited through template recursion so that every accumulator
 // index is a constant (a loop the compiler declined to unroll would index
-// the array at run time and move it to scratch memory).
-template <int EPI, int ACT, int FM, int FN, int B>
+// the array at run time and move it to scratch memory).  Column block q's 16
+// bias values are loaded once, before its FM blocks are stored: a load after
+// a store to C cannot be moved ahead of it (C might alias the bias), so
+// loading them per 32x32 block made every block wait a memory round trip
+// (15 us per 256x256 tile).
+template <int EPI, int ACT, int FM, int FN, int Q, int I>
+__device__ __forceinline__ void store_rows_t(const GemmArgs& p, f32x16 (&acc)[FM][FN], int64_t mb, int64_t nq,
+                                             const float (&bv)[16], bool vec, int lane) {
+    if constexpr (I < FM) {
+        store_block_t<EPI, ACT>(p, acc[I][Q], mb + 32 * I + (lane & 31), nq, bv, vec, lane >> 5);
+        store_rows_t<EPI, ACT, FM, FN, Q, I + 1>(p, acc, mb, nq, bv, vec, lane);
+    }
+}
+
+template <int EPI, int ACT, int FM, int FN, int Q>
 __device__ __forceinline__ void store_blocks_t(const GemmArgs& p, f32x16 (&acc)[FM][FN], int64_t mb, int64_t nb,
                                                bool vec, int lane) {
-    if constexpr (B < FM * FN) {
-        constexpr int q = B / FM, i = B % FM;
+    if constexpr (Q < FN) {
         const int h = lane >> 5;
-        const int64_t nq = nb + 32 * q;
+        const int64_t nq = nb + 32 * Q;
         float bv[16];
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
             const int64_t n = nq + 8 * (v >> 2) + 4 * h + (v & 3);
             bv[v] = (EPI == 1 && p.bias != nullptr && n < p.N) ? p.bias[n] : 0.0f;
         }
-        store_block_t<EPI, ACT>(p, acc[i][q], mb + 32 * i + (lane & 31), nq, bv, vec, h);
-        store_blocks_t<EPI, ACT, FM, FN, B + 1>(p, acc, mb, nb, vec, lane);
+        store_rows_t<EPI, ACT, FM, FN, Q, 0>(p, acc, mb, nq, bv, vec, lane);
+        store_blocks_t<EPI, ACT, FM, FN, Q + 1>(p, acc, mb, nb, vec, lane);
     }
 }
 
