@@ -156,11 +156,11 @@ int forced_split(const GemmArgs& a, const Tile* t) {
 // Sets *unsupported when the calling thread forced a direct tile this
 // problem cannot use; *split receives the split-K factor (1: none).
 // Size heuristic (measured on MI355X over the 1024..16384 sweep shapes):
-// 256x256 tiles when they give at least 256 blocks (one per CU); else 128x128 tiles (split
-// into parts at least 512 deep up to 512 blocks, two per CU, when they give
-// fewer than 256 blocks) when they give 128 blocks by themselves or, for
-// K >= 2048, with the split; else the
-// register-staged kernels (best for a 1024^3-sized problem).
+//  - 256x256 tiles when they give at least 256 blocks (one per CU);
+//  - else 128x128 tiles when they give at least 128 blocks, or for K >= 2048
+//    when split-K brings them there; below 256 blocks the k range is split
+//    into parts at least 512 deep, up to 512 blocks (two per CU);
+//  - else the register-staged kernels (best for a 1024^3-sized problem).
 const Tile* choose_bf16_direct(Kind kind, const GemmArgs& a, bool* unsupported, int* split) {
     *unsupported = false;
     *split = 1;
