@@ -13,6 +13,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr int kMaxPerLane = 32;  // C <= 2048
@@ -126,6 +128,34 @@ __device__ __forceinline__ void sgd_body(void* __restrict__ w, const float* __re
                                          int64_t block) {
 #pragma clang fp contract(off)
     const int64_t i0 = (block * kThreads + threadIdx.x) * 4;
+    // Four elements per thread: one 16-byte gradient load and one 8-byte
+    // (bf16) or 16-byte (fp32) weight load and store when aligned and whole.
+    const bool vec = i0 + 4 <= n && ((uintptr_t)g & 15) == 0 && ((uintptr_t)w & (BF16 ? 7 : 15)) == 0;
+    if (vec) {
+        const f32x4 gv = *(const f32x4*)(g + i0);
+        if (BF16) {
+            unsigned short* p = (unsigned short*)w + i0;
+            const uint2 wv = *(const uint2*)p;
+            const uint32_t h[4] = {wv.x & 0xffffu, wv.x >> 16, wv.y & 0xffffu, wv.y >> 16};
+            uint32_t o[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float step = lr * gv[e];
+                o[e] = to_bf16(__uint_as_float(h[e] << 16) - step);
+            }
+            *(uint2*)p = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
+        } else {
+            f32x4* p = (f32x4*)((float*)w + i0);
+            f32x4 wv = *p;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float step = lr * gv[e];
+                wv[e] = wv[e] - step;
+            }
+            *p = wv;
+        }
+        return;
+    }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const int64_t i = i0 + e;

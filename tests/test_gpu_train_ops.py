@@ -159,3 +159,25 @@ def test_sgd_update_multi(gpu, stream):
     for wb, g, t in zip(wbs, gs, tbs):
         got = t.cpu().numpy().view(np.uint16)
         assert np.array_equal(got, O.sgd_update(wb, g, lr))
+
+
+def test_sgd_update_unaligned(gpu, stream):
+    # Pointers one element past a 16-byte boundary take the element-wise
+    # path; the result is the same as the aligned vector path's.
+    n = 1029
+    w = O.normal(600, n + 1)
+    g = O.normal(601, n + 1)
+    lr = 0.07
+    dw, dg = dev(w), dev(g)
+    N.sgd_update(N.F32, ptr(dw) + 4, ptr(dg) + 4, lr, n, stream)
+    want = w.copy()
+    want[1:] = O.sgd_update(w[1:], g[1:], lr)
+    same_bits(host(dw), want)
+    wb = O.pack_bf16(w)
+    tb = torch.from_numpy(wb.view(np.int16).copy()).to("cuda:0")
+    N.sgd_update(N.BF16, ptr(tb) + 2, ptr(dg) + 4, lr, n, stream)
+    torch.cuda.synchronize()
+    got = tb.cpu().numpy().view(np.uint16)
+    wantb = wb.copy()
+    wantb[1:] = O.sgd_update(wb[1:], g[1:], lr)
+    assert np.array_equal(got, wantb)
