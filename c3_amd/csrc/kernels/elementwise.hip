@@ -20,11 +20,14 @@
 // exp, log and tanh are the device library's expf, logf, tanhf.
 //
 // Layout: flat contiguous fp32 arrays.  Fast path: one 16-byte vector per
-// operand per thread and a block per 256 vectors, non-temporal hints (the
-// data is touched once); measured on MI355X at 2^28 elements this shape
-// streams faster (6.4 TB/s for add) than 2, 4 or 8 vectors per thread or a
-// grid-stride loop.  The host picks the scalar kernel when n or a base
-// address is not 16-byte friendly.
+// operand per thread and a block per 128 vectors, non-temporal hints on
+// loads and stores (the data is touched once).  Measured on MI355X (add,
+// 2^28 elements): 128-thread blocks 6.70 TB/s, 256 6.44, 512 6.34, 1024
+// 6.40; two vectors per thread 6.04-6.15; a grid-stride loop 4.8-5.1;
+// plain loads 6.02-6.07 (non-temporal ones keep the streams out of the
+// caches).  At 2^24 (rotating operand sets) the block sizes tie at 6.3 TB/s.
+// The host picks the scalar kernel when n or a base address is not 16-byte
+// friendly.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -72,8 +75,9 @@ constexpr bool ew_binary() {
            OP == EW_SIGMOID_BWD || OP == EW_TANH_BWD || OP == EW_EXP_BWD;
 }
 
-constexpr int kThreads = 256;
-constexpr int kUnroll = 1;  // vectors per thread (must match the host grid)
+constexpr int kThreads = 256;     // scalar (grid-stride) kernels
+constexpr int kVecThreads = 128;  // vector kernels: one float4 per thread (must match the host grid)
+constexpr int kUnroll = 1;        // vectors per thread (must match the host grid)
 
 __device__ __forceinline__ f32x4 ld_nt(const f32x4* p) { return __builtin_nontemporal_load(p); }
 __device__ __forceinline__ void st_nt(f32x4 v, f32x4* p) { __builtin_nontemporal_store(v, p); }
@@ -82,11 +86,11 @@ __device__ __forceinline__ void st_nt(f32x4 v, f32x4* p) { __builtin_nontemporal
 template <int OP>
 __device__ __forceinline__ void ew_vec_body(const f32x4* __restrict__ a, const f32x4* __restrict__ b,
                                             float alpha, f32x4* __restrict__ out, int64_t n4, int64_t bmod4) {
-    const int64_t base = (int64_t)blockIdx.x * (kThreads * kUnroll) + threadIdx.x;
+    const int64_t base = (int64_t)blockIdx.x * (kVecThreads * kUnroll) + threadIdx.x;
     f32x4 va[kUnroll], vb[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-        const int64_t i = base + (int64_t)u * kThreads;
+        const int64_t i = base + (int64_t)u * kVecThreads;
         if (i < n4) {
             va[u] = ld_nt(a + i);
             if (ew_binary<OP>()) vb[u] = bmod4 > 0 ? b[i % bmod4] : ld_nt(b + i);
@@ -94,7 +98,7 @@ __device__ __forceinline__ void ew_vec_body(const f32x4* __restrict__ a, const f
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-        const int64_t i = base + (int64_t)u * kThreads;
+        const int64_t i = base + (int64_t)u * kVecThreads;
         if (i < n4) {
             f32x4 r;
 #pragma unroll
@@ -120,7 +124,7 @@ __device__ __forceinline__ void ew_scalar_body(const float* __restrict__ a, cons
 }
 
 #define C3_EW(NAME, OP)                                                                                  \
-    extern "C" __global__ __launch_bounds__(kThreads) void c3_ew_##NAME##_f32_v(                       \
+    extern "C" __global__ __launch_bounds__(kVecThreads) void c3_ew_##NAME##_f32_v(                    \
         const f32x4* a, const f32x4* b, float alpha, f32x4* out, int64_t n4, int64_t bmod4) {          \
         ew_vec_body<OP>(a, b, alpha, out, n4, bmod4);                                                   \
     }                                                                                                   \
@@ -177,8 +181,8 @@ __device__ __forceinline__ float chain_step(int node, float g, float x) {
 
 // One float4 per thread.  Every load of the element is issued before the
 // first store, so an output may alias an input at the same offsets.
-extern "C" __global__ __launch_bounds__(kThreads) void c3_bwd_chain_f32_v(ChainArgs p) {
-    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+extern "C" __global__ __launch_bounds__(kVecThreads) void c3_bwd_chain_f32_v(ChainArgs p) {
+    const int64_t i = (int64_t)blockIdx.x * kVecThreads + threadIdx.x;
     if (i >= p.n) return;
     f32x4 g = ld_nt((const f32x4*)p.g + i);
     f32x4 x[kChainMax];

@@ -66,6 +66,10 @@ struct Tile {
     int bk;  // k depth of one tile (direct-to-LDS kernels: K must be a multiple); 0 = any K
 };
 
+// Threads per block of the vector elementwise and backward-chain kernels
+// (elementwise.hip kVecThreads): one float4 per thread.
+constexpr int64_t kEwVecThreads = 128;
+
 const Tile kF32Tiles[] = {{"t64x64", 64, 64, 256}, {"t128x128", 128, 128, 256}, {"t256x128", 256, 128, 512}};
 const Tile kBf16Tiles[] = {{"t64x64", 64, 64, 256},
                            {"t128x128", 128, 128, 256},
@@ -81,10 +85,11 @@ const Tile* find_tile(const Tile* tiles, size_t n, const char* name) {
 // Tile forced for the calling thread (c3hip_set_gemm_tile); empty = none.
 thread_local std::string t_tile_f32, t_tile_bf16;
 
-// fp32 tile per GEMM kind and size (c3hip_set_gemm_tile, then C3_HIP_GEMM_TILE, override it).  Measured on MI355X at 8192x4096x4096:
-// the weight-gradient kinds (A read k-major, k = M = 8192 deep) run at
-// 121 TFLOP/s on 256x128 tiles against 112 on 128x128; forward and dX are
-// best on 128x128.  Small grids use 64x64 so every CU gets a block.
+// fp32 tile per GEMM kind and size (c3hip_set_gemm_tile, then C3_HIP_GEMM_TILE, override it).  Measured on MI355X at 8192x4096x4096
+// (tiles timed alternately in one process): the weight-gradient kinds (A read
+// k-major, k = M = 8192 deep) run at 121 TFLOP/s on 256x128 tiles against 112
+// on 128x128, the forward at 133 against 128.5; dX is best on 128x128 (119.5
+// against 116).  Small grids use 64x64 so every CU gets a block.
 const Tile* choose_f32_tile(Kind kind, int64_t M, int64_t N) {
     const size_t nt = sizeof(kF32Tiles) / sizeof(kF32Tiles[0]);
     const char* forced = !t_tile_f32.empty() ? t_tile_f32.c_str() : std::getenv("C3_HIP_GEMM_TILE");
@@ -93,7 +98,7 @@ const Tile* choose_f32_tile(Kind kind, int64_t M, int64_t N) {
     }
     const bool dw = kind == Kind::Dw || kind == Kind::DwMask;
     const int64_t blocks256 = ((M + 255) / 256) * ((N + 127) / 128);
-    if (dw && blocks256 >= 256) return &kF32Tiles[2];
+    if ((dw || kind == Kind::Fwd) && blocks256 >= 256) return &kF32Tiles[2];
     const int64_t blocks128 = ((M + 127) / 128) * ((N + 127) / 128);
     if (blocks128 >= 512) return &kF32Tiles[1];
     return &kF32Tiles[0];
@@ -548,11 +553,10 @@ int c3hip_elementwise(int op, int dtype, const void* a, const void* b, float alp
     if (vec) {
         std::snprintf(name, sizeof(name), "c3_ew_%s_f32_v", nm);
         int64_t n4 = n / 4, bmod4 = bmod / 4;
-        const int64_t per_block = 256;  // one vector per thread (elementwise.hip kUnroll)
-        const int64_t blocks = (n4 + per_block - 1) / per_block;
+        const int64_t blocks = (n4 + kEwVecThreads - 1) / kEwVecThreads;  // one vector per thread
         if (blocks > 0x7fffffff) return set_error(C3HIP_ERR_TOO_LARGE, "elementwise grid too large");
         void* args[] = {(void*)&a, (void*)&b, &alpha, &out, &n4, &bmod4};
-        return launch(name, dim3((unsigned)blocks), dim3(256), args, stream);
+        return launch(name, dim3((unsigned)blocks), dim3(kEwVecThreads), args, stream);
     }
     std::snprintf(name, sizeof(name), "c3_ew_%s_f32_s", nm);
     const int64_t blocks = std::min<int64_t>((n + 255) / 256, 1 << 16);
@@ -642,9 +646,9 @@ int c3hip_backward_chain(int dtype, const void* grad, const void* const* x, cons
     void* args[] = {&p};
     if (vec) {
         p.n = n / 4;
-        const int64_t blocks = (p.n + 255) / 256;  // one float4 per thread
+        const int64_t blocks = (p.n + kEwVecThreads - 1) / kEwVecThreads;  // one float4 per thread
         if (blocks > 0x7fffffff) return set_error(C3HIP_ERR_TOO_LARGE, "chain grid too large");
-        return launch("c3_bwd_chain_f32_v", dim3((unsigned)blocks), dim3(256), args, (hipStream_t)stream);
+        return launch("c3_bwd_chain_f32_v", dim3((unsigned)blocks), dim3(kEwVecThreads), args, (hipStream_t)stream);
     }
     p.n = n;
     const int64_t blocks = std::min<int64_t>((n + 255) / 256, 1 << 16);
