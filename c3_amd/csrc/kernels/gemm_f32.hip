@@ -324,3 +324,4 @@ __device__ __forceinline__ GemmArgs split_args_f32(const GemmArgs& p) {
 C3_GEMM_F32_KINDS(t64x64, 64, 64, 2, 2, 2)
 C3_GEMM_F32_KINDS(t128x128, 128, 128, 2, 2, 2)
 C3_GEMM_F32_KINDS(t256x128, 256, 128, 4, 2, 1)
+C3_GEMM_F32_KINDS(t128x256, 128, 256, 2, 4, 1)

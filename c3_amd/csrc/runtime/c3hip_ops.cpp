@@ -70,7 +70,8 @@ struct Tile {
 // (elementwise.hip kVecThreads): one float4 per thread.
 constexpr int64_t kEwVecThreads = 128;
 
-const Tile kF32Tiles[] = {{"t64x64", 64, 64, 256}, {"t128x128", 128, 128, 256}, {"t256x128", 256, 128, 512}};
+const Tile kF32Tiles[] = {{"t64x64", 64, 64, 256}, {"t128x128", 128, 128, 256}, {"t256x128", 256, 128, 512},
+                          {"t128x256", 128, 256, 512}};
 const Tile kBf16Tiles[] = {{"t64x64", 64, 64, 256},
                            {"t128x128", 128, 128, 256},
                            {"t256x128", 256, 128, 256},
@@ -86,10 +87,12 @@ const Tile* find_tile(const Tile* tiles, size_t n, const char* name) {
 thread_local std::string t_tile_f32, t_tile_bf16;
 
 // fp32 tile per GEMM kind and size (c3hip_set_gemm_tile, then C3_HIP_GEMM_TILE, override it).  Measured on MI355X at 8192x4096x4096
-// (tiles timed alternately in one process): the weight-gradient kinds (A read
-// k-major, k = M = 8192 deep) run at 121 TFLOP/s on 256x128 tiles against 112
-// on 128x128, the forward at 133 against 128.5; dX is best on 128x128 (119.5
-// against 116).  Small grids use 64x64 so every CU gets a block.
+// (tiles timed alternately in one process, TFLOP/s for 128x128 / 256x128 /
+// 128x256 / 256x256): forward 127-129 / 132-133 / 133 / 133; dX with the ReLU
+// mask 118-120 / 115-116 / 125-126 / 109; dW with mask and db 111-113 / 121-122
+// / 115-116 / 105.  dX stages two A operands (dY and Y for the mask), so the
+// tile that is wide in N loads the fewest of them per flop; dW reads A k-major
+// down k = M.  Small grids use 64x64 so every CU gets a block.
 const Tile* choose_f32_tile(Kind kind, int64_t M, int64_t N) {
     const size_t nt = sizeof(kF32Tiles) / sizeof(kF32Tiles[0]);
     const char* forced = !t_tile_f32.empty() ? t_tile_f32.c_str() : std::getenv("C3_HIP_GEMM_TILE");
@@ -97,7 +100,10 @@ const Tile* choose_f32_tile(Kind kind, int64_t M, int64_t N) {
         if (const Tile* t = find_tile(kF32Tiles, nt, forced)) return t;
     }
     const bool dw = kind == Kind::Dw || kind == Kind::DwMask;
+    const bool dx = kind == Kind::Dx || kind == Kind::DxMask;
     const int64_t blocks256 = ((M + 255) / 256) * ((N + 127) / 128);
+    const int64_t blocks_wide = ((M + 127) / 128) * ((N + 255) / 256);
+    if (dx && blocks_wide >= 256) return &kF32Tiles[3];
     if ((dw || kind == Kind::Fwd) && blocks256 >= 256) return &kF32Tiles[2];
     const int64_t blocks128 = ((M + 127) / 128) * ((N + 127) / 128);
     if (blocks128 >= 512) return &kF32Tiles[1];

@@ -49,7 +49,7 @@ def _kernel_symbols(hsaco: Path):
 def test_code_objects_hold_every_dispatched_kernel():
     gemm = _kernel_symbols(LIB / "gemm_f32.hsaco")
     for kind in ["fwd", "dx", "dx_mask", "dw", "dw_mask", "tt"]:
-        for tile in ["t64x64", "t128x128", "t256x128"]:
+        for tile in ["t64x64", "t128x128", "t256x128", "t128x256"]:
             for v in "vs":
                 assert f"c3_gemm_f32_{kind}_{tile}_{v}" in gemm
     ew = _kernel_symbols(LIB / "elementwise.hsaco")
@@ -130,7 +130,7 @@ def test_backward_chain_validation():
 
 
 def test_gemm_tile_override_validation():
-    assert native.gemm_tile_names(native.F32) == ["t64x64", "t128x128", "t256x128"]
+    assert native.gemm_tile_names(native.F32) == ["t64x64", "t128x128", "t256x128", "t128x256"]
     assert native.gemm_tile_names(native.BF16) == ["t64x64", "t128x128", "t256x128", "t256x256", "d256w8", "d256rq", "d256pp", "d128w4"]
     L = native.load()
     assert L.c3hip_set_gemm_tile(native.F32, b"d256w8") == native.ERR_INVALID  # a bf16-only tile

@@ -154,7 +154,7 @@ def _run_bwd(stream, X, W, Y, dY, act, want=("dX", "dW", "db")):
     return (None if dX is None else host(dX), None if dW is None else host(dW), None if db is None else host(db))
 
 
-@pytest.mark.parametrize("tile", ["t64x64", "t128x128", "t256x128"])
+@pytest.mark.parametrize("tile", ["t64x64", "t128x128", "t256x128", "t128x256"])
 @pytest.mark.parametrize("M,K,Nn", [(300, 260, 200), (257, 128, 64)])
 def test_every_fp32_tile_bit_exact(gpu, stream, monkeypatch, tile, M, K, Nn):
     # Each tile the planner can pick, forced for every GEMM of the layer
