@@ -419,12 +419,16 @@ def bench_mlp(torch, C, dev, s, dims, batch, dtype, steps, uniform_x, graph=Fals
     tr.close()
     del keep, x, xd, lbl
     torch.cuda.empty_cache()
-    flop = 6.0 * batch * sum(dims[l] * dims[l + 1] for l in range(len(dims) - 1))
+    # Forward 2·B·in·out per layer; backward dW 2·B·in·out per layer and dX
+    # 2·B·in·out for every layer but the first (the data batch needs no gradient).
+    macs = [batch * dims[l] * dims[l + 1] for l in range(len(dims) - 1)]
+    flop = 6.0 * sum(macs) - 2.0 * macs[0]
     tf = flop / (ms * 1e-3) / 1e12
     peak = PEAK_FP32_TFLOPS if dtype == C.F32 else PEAK_BF16_TFLOPS
     return {"dims": dims, "batch": batch, "dtype": "fp32" if dtype == C.F32 else "bf16",
             "ms_per_step": round(ms, 4), "us_per_step_wall": round(wall / steps * 1e6, 1),
             "tflops": round(tf, 3), "frac_of_peak": round(tf / peak, 4), "flop_per_step": flop,
+            "input_grad": "not computed for the first layer (its input is the data batch)",
             "warm_up_steps": warm, "region_hits_timed": st1["region_hits"] - st0["region_hits"],
             "backward_hits_timed": st1["backward_hits"] - st0["backward_hits"],
             "eager_ops_timed": st1["eager_ops"] - st0["eager_ops"],
@@ -487,12 +491,15 @@ def _cpu_mlp(O, np, reps=5):
             acts.append(O.linear_fwd(acts[-1], Ws[l], bs[l], 1 if l < 2 else 0))
         _, g = O.softmax_ce(acts[3], lbl)
         for l in reversed(range(3)):
-            g, dW, db = O.linear_bwd(acts[l], Ws[l], acts[l + 1], g, 1 if l < 2 else 0)
+            # Same work as the GPU step: no gradient for the data batch.
+            want = ("dX", "dW", "db") if l > 0 else ("dW", "db")
+            g, dW, db = O.linear_bwd(acts[l], Ws[l], acts[l + 1], g, 1 if l < 2 else 0, want=want)
             O.sgd_update(Ws[l], dW, 1e-3)
             O.sgd_update(bs[l], db, 1e-3)
         times.append(time.perf_counter() - t0)
     ms = sorted(times)[reps // 2] * 1e3
-    flop = 6.0 * B * sum(dims[l] * dims[l + 1] for l in range(3))
+    macs = [B * dims[l] * dims[l + 1] for l in range(3)]
+    flop = 6.0 * sum(macs) - 2.0 * macs[0]
     return {"ms_per_step": round(ms, 3), "tflops": round(flop / (ms * 1e-3) / 1e12, 6), "cores": 1,
             "kind": "port", "sample": f"median of {reps} full steps"}
 

@@ -123,11 +123,17 @@ public:
                                                           const std::vector<Tensor>& forward_inputs);
     // forward_inputs = {X, W, Y}; returns {dX, dW, db}.  act: C3HIP_ACT_* of
     // the layer (relu = true is C3HIP_ACT_RELU, false no activation).
+    // input_grad = false: the layer's input needs no gradient (autograd asks
+    // only for dW and db, e.g. the first layer of a network on data); dX is
+    // then not computed and comes back as an empty tensor, under its own key
+    // ("...|fused|nodx").
     std::optional<std::vector<Tensor>> tryExecuteLinearBackward(const Tensor& grad,
-                                                                const std::vector<Tensor>& forward_inputs, int act);
+                                                                const std::vector<Tensor>& forward_inputs, int act,
+                                                                bool input_grad = true);
     std::optional<std::vector<Tensor>> tryExecuteLinearBackward(const Tensor& grad,
-                                                                const std::vector<Tensor>& forward_inputs, bool relu) {
-        return tryExecuteLinearBackward(grad, forward_inputs, relu ? 1 : 0);
+                                                                const std::vector<Tensor>& forward_inputs, bool relu,
+                                                                bool input_grad = true) {
+        return tryExecuteLinearBackward(grad, forward_inputs, relu ? 1 : 0, input_grad);
     }
 
     static bool supportsNodeType(const std::string& node_type);

@@ -124,6 +124,7 @@ struct KernelSpec {
     int ew_op = 0;                                // C3HIP_EW_* for Elementwise
     float alpha = 1.0f;                           // scale factor of EW_SCALE
     int act = 0;                                  // C3HIP_ACT_* for LinearFwd / LinearBwd
+    bool input_grad = true;                       // LinearBwd: compute dX (false: the layer input needs no gradient)
     bool transA = false, transB = false;          // MatMul
     int axis = 0;                                 // SumReduce
     std::vector<int> chain;                       // C3HIP_CHAIN_* per node, BackwardChain

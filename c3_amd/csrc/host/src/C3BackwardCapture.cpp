@@ -209,7 +209,7 @@ std::optional<std::vector<Tensor>> C3BackwardCapture::tryExecuteBackward(const s
 
 std::optional<std::vector<Tensor>> C3BackwardCapture::tryExecuteLinearBackward(const Tensor& grad,
                                                                                const std::vector<Tensor>& fwd,
-                                                                               int act) {
+                                                                               int act, bool input_grad) {
     if (!backwardFusionEnabled()) return std::nullopt;
     if (fwd.size() != 3 || !deviceSupported(grad.device())) {
         unsupported_++;
@@ -220,7 +220,9 @@ std::optional<std::vector<Tensor>> C3BackwardCapture::tryExecuteLinearBackward(c
         return std::nullopt;
     }
     static const char* const kNames[] = {"Linear", "Linear+ReLU", "Linear+Sigmoid", "Linear+Tanh"};
-    const std::string key = makeBaseKey(kNames[act], grad, fwd) + "|fused";
+    // Without the input gradient (a layer whose input is the data) the
+    // kernel is a different one: its own key, output 0 empty.
+    const std::string key = makeBaseKey(kNames[act], grad, fwd) + (input_grad ? "|fused" : "|fused|nodx");
     // Graph inputs [dY, X, W, Y]: forward_inputs {X, W, Y} in order.
     auto r = C3KernelRegistry::getInstance().tryExecuteBackward(key, grad, fwd);
     if (r && r->size() == 3) {
@@ -240,6 +242,7 @@ std::optional<std::vector<Tensor>> C3BackwardCapture::tryExecuteLinearBackward(c
     if (act == C3HIP_ACT_SIGMOID) s.op_seq.push_back(op::Sigmoid);
     if (act == C3HIP_ACT_TANH) s.op_seq.push_back(op::Tanh);
     s.act = act;
+    s.input_grad = input_grad;
     s.dtype = X.dtype();
     s.input_shapes = {grad.shape(), X.shape(), W.shape(), fwd[2].shape()};
     s.out_shape = X.shape();

@@ -80,6 +80,7 @@ std::string KernelSpec::toString() const {
         for (int c : chain) ss << c << ",";
     }
     if (!tile.empty()) ss << "|tile=" << tile;
+    if (kind == KernelKind::LinearBwd && !input_grad) ss << "|nodx";
     ss << "|in=";
     for (const auto& s : input_shapes) ss << shapeToString(s) << ";";
     ss << "|out=" << shapeToString(out_shape);
@@ -107,7 +108,9 @@ std::vector<std::pair<std::vector<size_t>, DType>> KernelSpec::outputDescs() con
             const auto& X = input_shapes[1];
             const auto& W = input_shapes[2];
             if (X.size() != 2 || W.size() != 2) return {};
-            return {{X, dtype}, {{X[1], W[1]}, DType::kFloat}, {{W[1]}, DType::kFloat}};
+            // Without the input gradient output 0 is an empty tensor (shape {0}).
+            return {{input_grad ? X : std::vector<size_t>{0}, dtype}, {{X[1], W[1]}, DType::kFloat},
+                    {{W[1]}, DType::kFloat}};
         }
         case KernelKind::BackwardChain: {
             std::vector<std::pair<std::vector<size_t>, DType>> o;

@@ -198,15 +198,15 @@ std::vector<Tensor> HipCompiledKernel::execute(const std::vector<Tensor>& in) {
             return {out};
         }
         case KernelKind::LinearBwd: {
-            need(4);  // [dY, X, W, Y] -> [dX, dW, db]
+            need(4);  // [dY, X, W, Y] -> [dX, dW, db]; dX empty when the spec asks for no input gradient
             const Tensor &dY = in[0], &X = in[1], &W = in[2], &Y = in[3];
             const size_t M = X.shape()[0], K = X.shape()[1], N = W.shape()[1];
-            Tensor dX(ShapeTag{}, {M, K}, X.dtype(), DeviceType::kHIP);
+            Tensor dX = s.input_grad ? Tensor(ShapeTag{}, {M, K}, X.dtype(), DeviceType::kHIP) : Tensor();
             Tensor dW(ShapeTag{}, {K, N}, DType::kFloat, DeviceType::kHIP);
             Tensor db(ShapeTag{}, {N}, DType::kFloat, DeviceType::kHIP);
-            check(c3hip_linear_bwd(hipDtype(X.dtype()), X.data(), W.data(), Y.data(), dY.data(), dX.data(),
-                                   dW.data_ptr<float>(), db.data_ptr<float>(), (int64_t)M, (int64_t)K, (int64_t)N,
-                                   s.act, st),
+            check(c3hip_linear_bwd(hipDtype(X.dtype()), X.data(), W.data(), Y.data(), dY.data(),
+                                   s.input_grad ? dX.data() : nullptr, dW.data_ptr<float>(), db.data_ptr<float>(),
+                                   (int64_t)M, (int64_t)K, (int64_t)N, s.act, st),
                   "c3hip_linear_bwd");
             return {dX, dW, db};
         }

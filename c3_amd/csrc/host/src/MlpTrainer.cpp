@@ -184,10 +184,12 @@ float MlpTrainer::step(const Tensor& X, const void* labels, float lr, bool want_
     std::vector<Tensor> dWs(L), dbs(L);
     for (size_t i = L; i-- > 0;) {
         const bool relu = i + 1 < L;
+        // The first layer's input is the data batch: no gradient for it.
+        const bool input_grad = i > 0;
         const Tensor& A = acts_[i];
         const Tensor& Y = acts_[i + 1];
         Tensor dA, dW, db;
-        auto r = B.tryExecuteLinearBackward(g, {A, W_[i], Y}, relu);
+        auto r = B.tryExecuteLinearBackward(g, {A, W_[i], Y}, relu, input_grad);
         if (r && r->size() == 3) {
             dA = hold((*r)[0]);
             dW = hold((*r)[1]);
@@ -196,12 +198,12 @@ float MlpTrainer::step(const Tensor& X, const void* labels, float lr, bool want_
             step_bwd_hits_++;
         } else {
             const size_t M = A.shape()[0], K = dims_[i], N = dims_[i + 1];
-            dA = make({M, K}, dt_);
+            if (input_grad) dA = make({M, K}, dt_);
             dW = make({K, N}, DType::kFloat);
             db = make({N}, DType::kFloat);
-            check(c3hip_linear_bwd(hipDtype(dt_), A.data(), W_[i].data(), Y.data(), g.data(), dA.data(),
-                                   dW.data_ptr<float>(), db.data_ptr<float>(), (int64_t)M, (int64_t)K, (int64_t)N,
-                                   relu ? C3HIP_ACT_RELU : C3HIP_ACT_NONE, st),
+            check(c3hip_linear_bwd(hipDtype(dt_), A.data(), W_[i].data(), Y.data(), g.data(),
+                                   input_grad ? dA.data() : nullptr, dW.data_ptr<float>(), db.data_ptr<float>(),
+                                   (int64_t)M, (int64_t)K, (int64_t)N, relu ? C3HIP_ACT_RELU : C3HIP_ACT_NONE, st),
                   "eager linear backward");
             stats_.backward_misses++;
         }

@@ -696,6 +696,40 @@ TEST(backward_capture_rules_and_keys) {
     CHECK(st.cache_hit_count == 3 && st.cache_miss_count == 3 && st.compiles_submitted == 5);
 }
 
+// A layer whose input needs no gradient (the first layer on a data batch):
+// its fused backward is a different kernel (spec input_grad = false, "|nodx"
+// in the cache text and the registry key) whose output 0 is empty.
+TEST(linear_backward_without_input_grad) {
+    HostBackend hb;
+    KernelSpec seen;
+    int built_bwd = 0;
+    C3Engine::getInstance().setFactoryForTest([&](const KernelSpec& s, const CompileOptions& o) {
+        if (s.kind == KernelKind::LinearBwd) {
+            seen = s;
+            built_bwd++;
+        }
+        return std::make_shared<HostKernel>(s, o.opt_level);
+    });
+    auto& B = C3BackwardCapture::getInstance();
+    Tensor g = host({2, 2}, {1, -2, 3, -4});
+    Tensor X = host({2, 3}, {1, 0, 2, 0, 1, 0}), W = host({3, 2}, {1, 2, 3, 4, 5, 6}), Y = host({2, 2}, {1, 0, 2, 3});
+    CHECK(!B.tryExecuteLinearBackward(g, {X, W, Y}, true, false).has_value());
+    B.waitForPendingCompiles();
+    CHECK_EQ(built_bwd, 1);
+    CHECK(!seen.input_grad && seen.act == C3HIP_ACT_RELU);
+    CHECK(seen.toString().find("|nodx") != std::string::npos);
+    KernelSpec with = seen;
+    with.input_grad = true;
+    CHECK(with.toString().find("|nodx") == std::string::npos);
+    const auto d = seen.outputDescs();
+    CHECK(d.size() == 3 && d[0].first == std::vector<size_t>{0} && d[1].first == (std::vector<size_t>{3, 2}) &&
+          d[2].first == std::vector<size_t>{2});
+    CHECK(with.outputDescs()[0].first == (std::vector<size_t>{2, 3}));
+    const std::string base = C3BackwardCapture::makeBaseKey("Linear+ReLU", g, {X, W, Y});
+    CHECK(C3KernelRegistry::getInstance().hasBackwardKey(base + "|fused|nodx"));
+    CHECK(!C3KernelRegistry::getInstance().hasBackwardKey(base + "|fused"));
+}
+
 // ---------------------------------------------------- merged kernels, PGO --
 namespace {
 KernelSpec linearSpec(size_t M, size_t K, size_t N, int act) {
