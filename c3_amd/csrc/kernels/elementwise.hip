@@ -20,14 +20,14 @@
 // exp, log and tanh are the device library's expf, logf, tanhf.
 //
 // Layout: flat contiguous fp32 arrays.  Fast path: one 16-byte vector per
-// operand per thread and a block per 128 vectors, non-temporal hints on
-// loads and stores (the data is touched once).  Measured on MI355X (add,
-// 2^28 elements): 128-thread blocks 6.70 TB/s, 256 6.44, 512 6.34, 1024
-// 6.40; two vectors per thread 6.04-6.15; a grid-stride loop 4.8-5.1;
-// plain loads 6.02-6.07 (non-temporal ones keep the streams out of the
-// caches).  At 2^24 (rotating operand sets) the block sizes tie at 6.3 TB/s.
-// The host picks the scalar kernel when n or a base address is not 16-byte
-// friendly.
+// operand per thread and one wave (64 threads) per block, non-temporal hints
+// on loads and stores (the data is touched once).  Measured on MI355X,
+// variants timed alternately in one process on random data: add at 2^28,
+// 64-thread blocks 6.62 TB/s, 128 6.43-6.49, 256 5.99; scale at 2^24 with
+// rotating operand sets 6.19 against 5.84 (128 and 256) and 5.94 (512); two
+// or four vectors per thread, grid-stride loops and plain (cached) loads
+// were all slower.  The host picks the scalar kernel when n or a base
+// address is not 16-byte friendly.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -76,7 +76,7 @@ constexpr bool ew_binary() {
 }
 
 constexpr int kThreads = 256;     // scalar (grid-stride) kernels
-constexpr int kVecThreads = 128;  // vector kernels: one float4 per thread (must match the host grid)
+constexpr int kVecThreads = 64;   // vector kernels: one float4 per thread (must match the host grid)
 constexpr int kUnroll = 1;        // vectors per thread (must match the host grid)
 
 __device__ __forceinline__ f32x4 ld_nt(const f32x4* p) { return __builtin_nontemporal_load(p); }

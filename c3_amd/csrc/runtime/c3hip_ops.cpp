@@ -68,7 +68,7 @@ struct Tile {
 
 // Threads per block of the vector elementwise and backward-chain kernels
 // (elementwise.hip kVecThreads): one float4 per thread.
-constexpr int64_t kEwVecThreads = 128;
+constexpr int64_t kEwVecThreads = 64;
 
 const Tile kF32Tiles[] = {{"t64x64", 64, 64, 256}, {"t128x128", 128, 128, 256}, {"t256x128", 256, 128, 512},
                           {"t128x256", 128, 256, 512}};

@@ -228,3 +228,27 @@ def test_gpu_sum_reduce_golden(gpu, stream, axis):
     N.sum_reduce(ptr(dev(x)), ptr(out), M, Nn, axis, stream)
     torch.cuda.synchronize()
     same_bits(host(out), z[f"axis{axis}"])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
+def test_gpu_linear_empty_inner_dimension(gpu, stream, dtype):
+    """K = 0: the k-sum is empty, so Y = act(0 + b) and the backward's only
+    non-empty output is db = column sum of mask(Y) * dY (dX is M x 0, dW 0 x N)."""
+    import torch
+
+    from c3_amd import native as N
+    from tests.parity import dev, dev_bf16, empty, host, ptr
+
+    M, K, Nn = 40, 0, 24
+    b = ((np.arange(Nn) - 11.5) / 4).astype(np.float32)   # multiples of 1/8: exact in bf16
+    dY = np.random.default_rng(7).integers(-2, 3, size=(M, Nn)).astype(np.float32)
+    dt, tdt, up = (N.F32, torch.float32, dev) if dtype == "fp32" else (N.BF16, torch.bfloat16, dev_bf16)
+    Y = empty((M, Nn), dtype=tdt)
+    N.linear_fwd(dt, None, None, ptr(dev(b)), ptr(Y), M, K, Nn, N.ACT_RELU, stream)
+    db = empty(Nn)
+    N.linear_bwd(dt, None, None, ptr(Y), ptr(up(dY)), None, None, ptr(db), M, K, Nn, N.ACT_RELU, stream)
+    torch.cuda.synchronize()
+    ref_y = np.broadcast_to(np.maximum(b, 0), (M, Nn))
+    same_bits(host(Y), ref_y)            # b's values are exact in bf16
+    same_bits(host(db), ((b > 0).astype(np.float32) * dY).sum(0).astype(np.float32))
