@@ -257,23 +257,39 @@ __device__ __forceinline__ void gemm_f32_body(const GemmArgs& p) {
     // Epilogue: bias add then activation, straight from the accumulators.
     float* __restrict__ C = (float*)p.C;
     const int r = lane & 31, g = lane >> 5;
+    auto store_all = [&](auto actf) {
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-        const int64_t n = n0 + wn * TN + 32 * j + r;
-        const bool nok = n < p.N;
-        const float bv = (p.bias != nullptr && nok) ? p.bias[n] : 0.0f;
+        for (int j = 0; j < FN; ++j) {
+            const int64_t n = n0 + wn * TN + 32 * j + r;
+            const bool nok = n < p.N;
+            const float bv = (p.bias != nullptr && nok) ? p.bias[n] : 0.0f;
 #pragma unroll
-        for (int i = 0; i < FM; ++i) {
+            for (int i = 0; i < FM; ++i) {
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int64_t m = m0 + wm * TM + 32 * i + 8 * (v >> 2) + 4 * g + (v & 3);
-                if (nok && m < p.M) {
-                    float x = acc[i][j][v];
-                    if (p.bias != nullptr) x = x + bv;
-                    C[m * p.ldc + n] = act_apply(x, p.act);
+                for (int v = 0; v < 16; ++v) {
+                    const int64_t m = m0 + wm * TM + 32 * i + 8 * (v >> 2) + 4 * g + (v & 3);
+                    if (nok && m < p.M) {
+                        float x = acc[i][j][v];
+                        if (p.bias != nullptr) x = x + bv;
+                        C[m * p.ldc + n] = actf(x);
+                    }
                 }
             }
         }
+    };
+    if constexpr (BM * BN <= 64 * 64) {
+        // Small tiles run on grids of a few blocks, where each launch pays for
+        // fetching its code: the activation is chosen once per block so the
+        // stores carry only that activation's instructions (the per-element
+        // form puts the sigmoid and tanh code at each of the 16 stores).
+        with_act(p.act, [&](auto at) {
+            constexpr int ACT = decltype(at)::value;
+            store_all([](float x) { return act_c<ACT>(x); });
+        });
+    } else {
+        // Large tiles: the per-element form keeps the VGPR count (and so the
+        // occupancy) the MFMA loop needs.
+        store_all([&](float x) { return act_apply(x, p.act); });
     }
 }
 
