@@ -177,10 +177,9 @@ float MlpTrainer::step(const Tensor& X, const void* labels, float lr, bool want_
         kept_db_.clear();
     }
     auto& B = C3BackwardCapture::getInstance();
-    // Gradients of every layer; the SGD step runs once after the backward,
-    // one launch for the weights and one for the biases (every dA is formed
-    // from the old weights either way, so the result is the same as updating
-    // each layer as soon as its gradients exist).
+    // Gradients of every layer; the SGD step runs once after the backward
+    // (every dA is formed from the old weights either way, so the result is
+    // the same as updating each layer as soon as its gradients exist).
     std::vector<Tensor> dWs(L), dbs(L);
     for (size_t i = L; i-- > 0;) {
         const bool relu = i + 1 < L;
@@ -216,24 +215,32 @@ float MlpTrainer::step(const Tensor& X, const void* labels, float lr, bool want_
         dbs[i] = db;
         g = dA;
     }
-    for (size_t i0 = 0; i0 < L; i0 += C3HIP_SGD_MAX_TENSORS) {
-        const size_t k = std::min<size_t>(C3HIP_SGD_MAX_TENSORS, L - i0);
-        void* w[C3HIP_SGD_MAX_TENSORS];
-        void* bb[C3HIP_SGD_MAX_TENSORS];
-        const float* gw[C3HIP_SGD_MAX_TENSORS];
-        const float* gb[C3HIP_SGD_MAX_TENSORS];
-        int64_t nw[C3HIP_SGD_MAX_TENSORS], nb[C3HIP_SGD_MAX_TENSORS];
-        for (size_t t = 0; t < k; ++t) {
-            w[t] = W_[i0 + t].data();
-            gw[t] = dWs[i0 + t].data_ptr<float>();
-            nw[t] = (int64_t)W_[i0 + t].numel();
-            bb[t] = b_[i0 + t].data();
-            gb[t] = dbs[i0 + t].data_ptr<float>();
-            nb[t] = (int64_t)b_[i0 + t].numel();
-        }
-        check(c3hip_sgd_update_multi(hipDtype(dt_), (int)k, w, gw, nw, lr, st), "sgd W");
-        check(c3hip_sgd_update_multi(C3HIP_F32, (int)k, bb, gb, nb, lr, st), "sgd b");
+    // fp32 weights: weights and biases share one launch (up to 16 tensors);
+    // bf16 weights: one launch for the weights, one for the fp32 biases.
+    // The same per-element update either way.
+    std::vector<void*> sw, sb;
+    std::vector<const float*> sgw, sgb;
+    std::vector<int64_t> snw, snb;
+    for (size_t i = 0; i < L; ++i) {
+        sw.push_back(W_[i].data());
+        sgw.push_back(dWs[i].data_ptr<float>());
+        snw.push_back((int64_t)W_[i].numel());
+        auto& bp = dt_ == DType::kFloat ? sw : sb;
+        auto& bg = dt_ == DType::kFloat ? sgw : sgb;
+        auto& bn = dt_ == DType::kFloat ? snw : snb;
+        bp.push_back(b_[i].data());
+        bg.push_back(dbs[i].data_ptr<float>());
+        bn.push_back((int64_t)b_[i].numel());
     }
+    auto sgd = [&](int dtype, std::vector<void*>& w, std::vector<const float*>& g, std::vector<int64_t>& n,
+                   const char* what) {
+        for (size_t i0 = 0; i0 < w.size(); i0 += C3HIP_SGD_MAX_TENSORS) {
+            const size_t k = std::min<size_t>(C3HIP_SGD_MAX_TENSORS, w.size() - i0);
+            check(c3hip_sgd_update_multi(dtype, (int)k, w.data() + i0, g.data() + i0, n.data() + i0, lr, st), what);
+        }
+    };
+    sgd(hipDtype(dt_), sw, sgw, snw, "sgd W");
+    if (!sb.empty()) sgd(C3HIP_F32, sb, sgb, snb, "sgd b");
     stats_.steps++;
     // Every ReLU layer as a region (MatMul+Add alone is below the cost
     // model's threshold and stays unfused) and every backward fused.

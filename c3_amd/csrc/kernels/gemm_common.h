@@ -39,12 +39,15 @@ struct GemmArgs {
 // Renumber so that consecutive logical tiles land on the same XCD and share
 // its L2, then walk tiles in groups of GROUP_M row-tiles so that a group's
 // A rows and B columns stay L2-resident.
+// bid: the block's index among this GEMM's blocks (blockIdx.x, or less an
+// offset when one launch runs the blocks of two GEMMs).
 template <int GROUP_M>
-__device__ __forceinline__ void tile_coords(int64_t M, int64_t N, int BM, int BN, int& tm, int& tn) {
+__device__ __forceinline__ void tile_coords(int64_t M, int64_t N, int BM, int BN, int& tm, int& tn,
+                                            int bid = -1) {
     const int nbm = (int)((M + BM - 1) / BM);
     const int nbn = (int)((N + BN - 1) / BN);
     const int nblk = nbm * nbn;
-    int bid = blockIdx.x;
+    if (bid < 0) bid = blockIdx.x;
     int id = bid;
     if ((nblk & 7) == 0) id = (bid & 7) * (nblk >> 3) + (bid >> 3);
     const int per_group = GROUP_M * nbn;

@@ -138,9 +138,10 @@ __device__ __forceinline__ void read_frag(const float* __restrict__ S, int r0, i
     }
 }
 
+// bid: this block's index among the GEMM's blocks (see tile_coords).
 template <int BM, int BN, int WAVES_M, int WAVES_N, bool AK, bool BKC, bool AMASK, bool BMASK,
           bool DB, bool VEC>
-__device__ __forceinline__ void gemm_f32_body(const GemmArgs& p) {
+__device__ __forceinline__ void gemm_f32_body(const GemmArgs& p, int bid) {
     constexpr int NT = 64 * WAVES_M * WAVES_N;
     constexpr int TM = BM / WAVES_M, TN = BN / WAVES_N;
     constexpr int FM = TM / 32, FN = TN / 32;
@@ -157,7 +158,7 @@ __device__ __forceinline__ void gemm_f32_body(const GemmArgs& p) {
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
 
     int tm, tn;
-    tile_coords<8>(p.M, p.N, BM, BN, tm, tn);
+    tile_coords<8>(p.M, p.N, BM, BN, tm, tn, bid);
     const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
 
     const float* __restrict__ A = (const float*)p.A;
@@ -320,11 +321,11 @@ __device__ __forceinline__ GemmArgs split_args_f32(const GemmArgs& p) {
 // Tile suffix _tBMxBN_wWMxWN; _v: vectorised operand loads (contiguous extent
 // % 4 == 0 and 16-byte aligned bases), _s: scalar loads.
 #define C3_GEMM_F32_ONE(NAME, BM, BN, WM, WN, OCC, AK, BKC, AMASK, BMASK, DB)                         \
-    extern "C" __global__ __launch_bounds__(64 * WM * WN, OCC) void NAME##_v(GemmArgs p) {           \
-        gemm_f32_body<BM, BN, WM, WN, AK, BKC, AMASK, BMASK, DB, true>(split_args_f32<AK, BKC>(p));  \
-    }                                                                                               \
-    extern "C" __global__ __launch_bounds__(64 * WM * WN, OCC) void NAME##_s(GemmArgs p) {           \
-        gemm_f32_body<BM, BN, WM, WN, AK, BKC, AMASK, BMASK, DB, false>(split_args_f32<AK, BKC>(p)); \
+    extern "C" __global__ __launch_bounds__(64 * WM * WN, OCC) void NAME##_v(GemmArgs p) {                     \
+        gemm_f32_body<BM, BN, WM, WN, AK, BKC, AMASK, BMASK, DB, true>(split_args_f32<AK, BKC>(p), blockIdx.x);  \
+    }                                                                                                         \
+    extern "C" __global__ __launch_bounds__(64 * WM * WN, OCC) void NAME##_s(GemmArgs p) {                     \
+        gemm_f32_body<BM, BN, WM, WN, AK, BKC, AMASK, BMASK, DB, false>(split_args_f32<AK, BKC>(p), blockIdx.x); \
     }
 
 // Kinds: fwd (A=X k-contig, B=W [K,N]); dx/dx_mask (A=dY[, masked by Y], B=W as [N][K]);
@@ -341,3 +342,29 @@ C3_GEMM_F32_KINDS(t64x64, 64, 64, 2, 2, 2)
 C3_GEMM_F32_KINDS(t128x128, 128, 128, 2, 2, 2)
 C3_GEMM_F32_KINDS(t256x128, 256, 128, 4, 2, 1)
 C3_GEMM_F32_KINDS(t128x256, 128, 256, 2, 4, 1)
+
+// The whole layer backward of a small layer in one launch: blocks
+// [0, nx) compute dX = dZ . W^T (dx kind), blocks [nx, nx + nw) dW = X^T . dZ
+// with db (dw kind), each with its own tile walk; a block runs one of the
+// two bodies, so results are those of the two separate launches.  For grids
+// of a few 64x64 tiles, where each launch costs more than its k-loop.
+struct BwdPairArgs {
+    GemmArgs dx;
+    GemmArgs dw;
+    int nx;
+    int _pad;
+};
+
+#define C3_GEMM_F32_BWD_PAIR(NAME, BM, BN, WM, WN, OCC, MASK, VEC)                                              \
+    extern "C" __global__ __launch_bounds__(64 * WM * WN, OCC) void NAME(BwdPairArgs p) {                      \
+        const int b = blockIdx.x;                                                                              \
+        if (b < p.nx)                                                                                          \
+            gemm_f32_body<BM, BN, WM, WN, true, true, MASK, false, false, VEC>(p.dx, b);                      \
+        else                                                                                                   \
+            gemm_f32_body<BM, BN, WM, WN, false, false, false, MASK, true, VEC>(p.dw, b - p.nx);              \
+    }
+
+C3_GEMM_F32_BWD_PAIR(c3_gemm_f32_bwd_t64x64_v, 64, 64, 2, 2, 2, false, true)
+C3_GEMM_F32_BWD_PAIR(c3_gemm_f32_bwd_t64x64_s, 64, 64, 2, 2, 2, false, false)
+C3_GEMM_F32_BWD_PAIR(c3_gemm_f32_bwd_mask_t64x64_v, 64, 64, 2, 2, 2, true, true)
+C3_GEMM_F32_BWD_PAIR(c3_gemm_f32_bwd_mask_t64x64_s, 64, 64, 2, 2, 2, true, false)

@@ -44,6 +44,15 @@ struct GemmArgs {
     int64_t c_split;
 };
 
+// Argument block of c3_gemm_f32_bwd[_mask]_t64x64_* (mirrors BwdPairArgs in
+// gemm_f32.hip): blocks [0, nx) run dx, the rest dw.
+struct BwdPairArgs {
+    GemmArgs dx;
+    GemmArgs dw;
+    int nx;
+    int _pad;
+};
+
 // Argument block of c3_sgd_multi_* (mirrors SgdMultiArgs in
 // c3_amd/csrc/kernels/loss.hip).
 struct SgdMultiArgs {

@@ -93,6 +93,8 @@ thread_local std::string t_tile_f32, t_tile_bf16;
 // / 115-116 / 105.  dX stages two A operands (dY and Y for the mask), so the
 // tile that is wide in N loads the fewest of them per flop; dW reads A k-major
 // down k = M.  Small grids use 64x64 so every CU gets a block.
+bool f32_forced() { return !t_tile_f32.empty() || std::getenv("C3_HIP_GEMM_TILE") != nullptr; }
+
 const Tile* choose_f32_tile(Kind kind, int64_t M, int64_t N) {
     const size_t nt = sizeof(kF32Tiles) / sizeof(kF32Tiles[0]);
     const char* forced = !t_tile_f32.empty() ? t_tile_f32.c_str() : std::getenv("C3_HIP_GEMM_TILE");
@@ -700,6 +702,31 @@ int c3hip_linear_fwd(int dtype, const void* X, const void* W, const float* b, vo
     return run_gemm(dtype, Kind::Fwd, a, true, false, (hipStream_t)stream);
 }
 
+// Both GEMMs of a small fp32 layer backward in one launch (c3_gemm_f32_bwd*):
+// taken when each would run as a plain 64x64-tile launch of fewer than 64
+// tiles (no split-K, no forced tile), where a launch costs more than the
+// k-loop it carries.  Same blocks, tile walks and arithmetic as the two
+// separate launches.  C3HIP_ERR_UNSUPPORTED: not applicable, nothing launched.
+int linear_bwd_pair(const GemmArgs& ax, const GemmArgs& aw, bool relu, hipStream_t stream) {
+    const Kind kx = relu ? Kind::DxMask : Kind::Dx, kw = relu ? Kind::DwMask : Kind::Dw;
+    const Tile* t = &kF32Tiles[0];
+    if (f32_forced() || choose_f32_tile(kx, ax.M, ax.N) != t || choose_f32_tile(kw, aw.M, aw.N) != t ||
+        plan_split_f32(ax, t) || plan_split_f32(aw, t))
+        return C3HIP_ERR_UNSUPPORTED;
+    const int64_t nx = tile_count(ax, t), nw = tile_count(aw, t);
+    if (nx + nw > 128) return C3HIP_ERR_UNSUPPORTED;
+    const bool vec = vec_ok(true, ax.M, ax.K, ax.lda, ax.A, ax.Amask) && vec_ok(true, ax.N, ax.K, ax.ldb, ax.B, ax.Bmask) &&
+                     vec_ok(false, aw.M, aw.K, aw.lda, aw.A, aw.Amask) && vec_ok(false, aw.N, aw.K, aw.ldb, aw.B, aw.Bmask);
+    BwdPairArgs p{};
+    p.dx = ax;
+    p.dw = aw;
+    p.nx = (int)nx;
+    char name[64];
+    std::snprintf(name, sizeof(name), "c3_gemm_f32_bwd%s_t64x64_%s", relu ? "_mask" : "", vec ? "v" : "s");
+    void* args[] = {&p};
+    return launch(name, dim3((unsigned)(nx + nw)), dim3(t->threads), args, stream);
+}
+
 int c3hip_linear_bwd(int dtype, const void* X, const void* W, const void* Y, const void* dY, void* dX, float* dW,
                      float* db, int64_t M, int64_t K, int64_t N, int act, void* stream_) {
     clear_error();
@@ -715,21 +742,27 @@ int c3hip_linear_bwd(int dtype, const void* X, const void* W, const void* Y, con
     if (dtype == C3HIP_BF16 || act == C3HIP_ACT_SIGMOID || act == C3HIP_ACT_TANH)
         return linear_bwd_prepass(dtype, X, W, Y, dY, dX, dW, db, M, K, N, act, stream);
     const void* mask = relu ? Y : nullptr;
+    // dX[M,K] = dZ[M,N] . W^T : logical (M, N=K, K=N), A = dY (k-contig), B(k=n, j) = W[j*N + n].
+    GemmArgs ax{};
+    ax.A = dY; ax.Amask = mask; ax.B = W; ax.C = dX;
+    ax.M = M; ax.N = K; ax.K = N;
+    ax.lda = N; ax.ldb = N; ax.ldc = K;
+    // dW[K,N] = X^T . dZ : logical (M=K, N, K=M), A(i, m) = X[m*K + i], B(m, j) = dZ[m*N + j].
+    GemmArgs aw{};
+    aw.A = X; aw.B = dY; aw.Bmask = mask; aw.C = dW; aw.db = db;
+    aw.M = K; aw.N = N; aw.K = M;
+    aw.lda = K; aw.ldb = N; aw.ldc = N;
+    if (dX && dW && M > 0 && N > 0 && K > 0) {
+        rc = linear_bwd_pair(ax, aw, relu, stream);
+        if (rc != C3HIP_ERR_UNSUPPORTED) return rc;  // launched (or failed); unsupported: separate launches
+        clear_error();
+    }
     if (dX) {
-        // dX[M,K] = dZ[M,N] . W^T : logical (M, N=K, K=N), A = dY (k-contig), B(k=n, j) = W[j*N + n].
-        GemmArgs a{};
-        a.A = dY; a.Amask = mask; a.B = W; a.C = dX;
-        a.M = M; a.N = K; a.K = N;
-        a.lda = N; a.ldb = N; a.ldc = K;
-        rc = run_gemm(dtype, relu ? Kind::DxMask : Kind::Dx, a, true, true, stream);
+        rc = run_gemm(dtype, relu ? Kind::DxMask : Kind::Dx, ax, true, true, stream);
         if (rc) return rc;
     }
     if (dW) {
-        // dW[K,N] = X^T . dZ : logical (M=K, N, K=M), A(i, m) = X[m*K + i], B(m, j) = dZ[m*N + j].
-        GemmArgs a{};
-        a.A = X; a.B = dY; a.Bmask = mask; a.C = dW; a.db = db;
-        a.M = K; a.N = N; a.K = M;
-        a.lda = K; a.ldb = N; a.ldc = N;
+        GemmArgs& a = aw;
         if (K == 0 && db) {
             // No dW rows: no block would visit dY, so the column sums run on their own.
             a.db = nullptr;

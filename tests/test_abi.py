@@ -52,6 +52,8 @@ def test_code_objects_hold_every_dispatched_kernel():
         for tile in ["t64x64", "t128x128", "t256x128", "t128x256"]:
             for v in "vs":
                 assert f"c3_gemm_f32_{kind}_{tile}_{v}" in gemm
+    for name in ["c3_gemm_f32_bwd_t64x64", "c3_gemm_f32_bwd_mask_t64x64"]:
+        assert f"{name}_v" in gemm and f"{name}_s" in gemm
     ew = _kernel_symbols(LIB / "elementwise.hsaco")
     for op in list(native.EW_OPS) + list(native.EW_MATH_OPS):
         assert f"c3_ew_{op}_f32_v" in ew and f"c3_ew_{op}_f32_s" in ew

@@ -154,6 +154,22 @@ def _run_bwd(stream, X, W, Y, dY, act, want=("dX", "dW", "db")):
     return (None if dX is None else host(dX), None if dW is None else host(dW), None if db is None else host(db))
 
 
+@pytest.mark.parametrize("M,K,Nn,act", [(128, 256, 128, 1), (128, 128, 10, 0), (37, 70, 33, 1), (64, 300, 40, 1),
+                                          (200, 96, 130, 0)])
+def test_small_bwd_one_launch_matches_two(gpu, stream, monkeypatch, M, K, Nn, act):
+    # Small fp32 layers run dX and dW + db in one launch; forcing the 64x64
+    # tile takes the two separate launches of the same tile.  Real-valued
+    # inputs: the results must agree bit for bit (same tiles, same k order).
+    X, W, Y, dY = _bwd_inputs(71, M, K, Nn, False)
+    one = _run_bwd(stream, X, W, Y, dY, act)
+    monkeypatch.setenv("C3_HIP_GEMM_TILE", "t64x64")
+    two = _run_bwd(stream, X, W, Y, dY, act)
+    for g1, g2 in zip(one, two):
+        same_bits(g1, g2)
+    rX, rW, rb = O.linear_bwd(X, W, Y, dY, act)
+    assert_close_gemm(one[1], rW, gemm_bound(X.T, O.relu_mask_mul(Y, dY) if act else dY, M), FP32_TOL, what="dW")
+
+
 @pytest.mark.parametrize("tile", ["t64x64", "t128x128", "t256x128", "t128x256"])
 @pytest.mark.parametrize("M,K,Nn", [(300, 260, 200), (257, 128, 64)])
 def test_every_fp32_tile_bit_exact(gpu, stream, monkeypatch, tile, M, K, Nn):
