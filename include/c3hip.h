@@ -210,7 +210,9 @@ int c3hip_linear_fwd(int dtype, const void* X, const void* W, const float* b, vo
  *   dX[M,K] = dZ . W^T,  dW[K,N] = X^T . dZ,  db[N] = sum over rows of dZ.
  * dX, dW and db are each optional (NULL skips it).  dZ is formed inside the
  * GEMM operand loads and never written.  C3HIP_F32: all fp32.  C3HIP_BF16:
- * X, W, Y, dY and dX bf16; dW and db fp32.
+ * X, W, Y, dY and dX bf16; dW and db fp32.  Outputs must not overlap the
+ * inputs or each other: dX, dW and db may be computed by one launch (small
+ * fp32 layers), so no output is ordered before another's reads.
  * Replaces the per-node backward kernels the reference installs for one
  * layer: ReLU (Gt + Mul, src/C3/C3BackwardCapture.cpp:501-528), MatMul in:0
  * and in:1 (:681-723) and Add in:1 SumReduce (:618-644), looked up through
