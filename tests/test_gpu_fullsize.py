@@ -65,3 +65,47 @@ def test_fullsize_sampled_parity(gpu, stream, dtype):
     assert_close_gemm(host(dW)[:, COLS], ref_cols, gemm_bound(X.T, dZ[:, COLS], M), tol, what="dW cols")
     assert_close_gemm(host(db), O.sum_reduce(dZ, 0), 2.02 * M * 2.0 ** -24 * np.abs(dZ.astype(np.float64)).sum(0),
                       tol, what="db")
+
+
+def _bf16_rne(x):
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32).view(np.float32)
+
+
+@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
+def test_fullsize_integer_bit_exact(gpu, stream, dtype):
+    """Integer inputs in -2..2 at 8192x4096x4096: every partial sum is an
+    integer below 2^24, so any summation order gives the exact result.
+    Sampled rows of Y and dX, sampled columns of dW and all of db must equal
+    int64 arithmetic bit for bit (bf16: Y and dX rounded once to bf16)."""
+    bf = dtype == "bf16"
+    rng = np.random.default_rng(0xF5)
+    Xi = rng.integers(-2, 3, size=(M, K), dtype=np.int64)
+    Wi = rng.integers(-2, 3, size=(K, NN), dtype=np.int64)
+    bi = rng.integers(-2, 3, size=NN, dtype=np.int64)
+    dYi = rng.integers(-2, 3, size=(M, NN), dtype=np.int64)
+    f = lambda a: a.astype(np.float32)  # noqa: E731
+    up = dev_bf16 if bf else dev
+    tdt = torch.bfloat16 if bf else torch.float32
+    code = N.BF16 if bf else N.F32
+    X_, W_, dY_ = up(f(Xi)), up(f(Wi)), up(f(dYi))
+    Y = empty((M, NN), dtype=tdt)
+    N.linear_fwd(code, ptr(X_), ptr(W_), ptr(dev(f(bi))), ptr(Y), M, K, NN, N.ACT_RELU, stream)
+    dX = empty((M, K), dtype=tdt)
+    dW, db = empty((K, NN)), empty(NN)
+    N.linear_bwd(code, ptr(X_), ptr(W_), ptr(Y), ptr(dY_), ptr(dX), ptr(dW), ptr(db), M, K, NN, N.ACT_RELU, stream)
+    rnd = _bf16_rne if bf else (lambda a: a)
+    # Reference in float64 (BLAS): every product and partial sum is an integer
+    # far below 2^53, so float64 is exact in any order, like int64.
+    Xd, Wd, bd, dYd = (a.astype(np.float64) for a in (Xi, Wi, bi, dYi))
+
+    def bits_equal(got, ref, what):
+        bad = got.view(np.int32) != ref.view(np.int32)
+        assert not bad.any(), f"{what}: {int(bad.sum())} elements differ, first at {np.argwhere(bad)[:3].tolist()}"
+
+    Z = Xd @ Wd + bd                      # exact
+    dZ = (Z > 0) * dYd
+    bits_equal(host(Y)[ROWS], rnd(f(np.maximum(Z[ROWS], 0))), "Y rows")
+    bits_equal(host(dX)[ROWS], rnd(f(dZ[ROWS] @ Wd.T)), "dX rows")
+    bits_equal(host(dW)[:, COLS], f(Xd.T @ dZ[:, COLS]), "dW cols")
+    bits_equal(host(db), f(dZ.sum(0)), "db")
