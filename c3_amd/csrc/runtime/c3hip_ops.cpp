@@ -88,7 +88,7 @@ thread_local std::string t_tile_f32, t_tile_bf16;
 
 // fp32 tile per GEMM kind and size (c3hip_set_gemm_tile, then C3_HIP_GEMM_TILE, override it).  Measured on MI355X at 8192x4096x4096
 // (tiles timed alternately in one process, TFLOP/s for 128x128 / 256x128 /
-// 128x256 / 256x256): forward 127-129 / 132-133 / 133 / 133; dX with the ReLU
+// 128x256 / 256x256, the last measured and not built): forward 127-129 / 132-133 / 133 / 133; dX with the ReLU
 // mask 118-120 / 115-116 / 125-126 / 109; dW with mask and db 111-113 / 121-122
 // / 115-116 / 105.  dX stages two A operands (dY and Y for the mask), so the
 // tile that is wide in N loads the fewest of them per flop; dW reads A k-major
@@ -703,9 +703,9 @@ int c3hip_linear_fwd(int dtype, const void* X, const void* W, const float* b, vo
 }
 
 // Both GEMMs of a small fp32 layer backward in one launch (c3_gemm_f32_bwd*):
-// taken when each would run as a plain 64x64-tile launch of fewer than 64
-// tiles (no split-K, no forced tile), where a launch costs more than the
-// k-loop it carries.  Same blocks, tile walks and arithmetic as the two
+// taken when each would run as a plain 64x64-tile launch (no split-K, no
+// forced tile) and the two grids hold at most 128 tiles together, where a
+// launch costs more than the k-loop it carries.  Same blocks, tile walks and arithmetic as the two
 // separate launches.  C3HIP_ERR_UNSUPPORTED: not applicable, nothing launched.
 int linear_bwd_pair(const GemmArgs& ax, const GemmArgs& aw, bool relu, hipStream_t stream) {
     const Kind kx = relu ? Kind::DxMask : Kind::Dx, kw = relu ? Kind::DwMask : Kind::Dw;
