@@ -44,6 +44,9 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the evidence beside the headline (bf16 layer and sweep, elementwise, MLP steps)")
+    ap.add_argument("--elementwise-profile", action="store_true",
+                    help="only run each of the eight elementwise ops three times over 2^28 fp32 elements (random "
+                         "data), for rocprofv3 kernel-trace and FETCH_SIZE/WRITE_SIZE summaries of the streams")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain copy-like stream (scale: read 2^26 fp32, write 2^26 fp32) three times; "
                          "its FETCH_SIZE/WRITE_SIZE counters calibrate the HBM traffic figures")
@@ -67,6 +70,25 @@ def copy_calibration():
                                            "write_bytes": 4 * n, "launches": 3}}), flush=True)
 
 
+def elementwise_profile(n=1 << 28, reps=3):
+    import torch
+
+    from c3_amd import native as C
+
+    C.init(0)
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(0xE7)
+    a = torch.randn(n, device="cuda:0", generator=g)
+    b = torch.rand(n, device="cuda:0", generator=g) * 1.5 + 0.5
+    o = torch.empty(n, device="cuda:0")
+    s = torch.cuda.current_stream().cuda_stream
+    for name, code in C.EW_OPS.items():
+        for _ in range(reps):
+            C.elementwise(code, C.F32, a.data_ptr(), b.data_ptr(), 0.5, o.data_ptr(), n, 0, s)
+    torch.cuda.synchronize()
+    print(json.dumps({"elementwise_profile": {"n": n, "launches_per_op": reps, "ops": list(C.EW_OPS)}}), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -75,6 +97,9 @@ def main():
         sys.exit(2)
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.elementwise_profile:
+        elementwise_profile()
         return
 
     import torch
