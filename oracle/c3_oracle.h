@@ -10,6 +10,19 @@
  * All arithmetic is IEEE fp32, one rounding per operation, no fused
  * multiply-add (the file is compiled with -ffp-contract=off, without
  * -ffast-math), loops in the reference's order.  Matrices are row-major.
+ *
+ * How it is pinned (the reference holds no golden vectors and cannot be built
+ * here; tests/test_oracle.py and tests/test_golden.py): integer-valued inputs
+ * against exact arithmetic (all transpose cases, bias, mask, db, SumReduce);
+ * known-answer fixtures in tests/golden/ made by numpy alone (exact integer
+ * layers, single IEEE operations over special values, softmax-CE closed
+ * forms); float64 brute force within the gamma_K bound; hand-built cases
+ * that change if the summation order, FMA contraction, bias placement, mask
+ * sign or maxnum NaN rule change; closed forms and central differences for
+ * softmax-CE and SGD.  Parity unpinned: the exact bits of the reference's
+ * LLVM-JIT output, i.e. that LLVM neither reassociated nor contracted the
+ * sequential k-loop; this file follows the reference's source, and no check
+ * available here can observe its compiled code.
  */
 #ifndef C3_ORACLE_H
 #define C3_ORACLE_H

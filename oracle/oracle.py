@@ -4,7 +4,9 @@ TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
 bench.py's cpu_baseline leg, as the checker.  The product path never imports
 this module.
 
-Arrays are numpy float32 / int32, C-contiguous.
+Arrays are numpy float32 / int32, C-contiguous.  How each restated function
+is pinned, and the one property left "parity unpinned" (the exact bits of
+the reference's LLVM-JIT output), is stated in c3_oracle.h.
 """
 from __future__ import annotations
 
