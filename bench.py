@@ -45,8 +45,15 @@ def parse():
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the evidence beside the headline (bf16 layer and sweep, elementwise, MLP steps)")
     ap.add_argument("--elementwise-profile", action="store_true",
-                    help="only run each of the eight elementwise ops three times over 2^28 fp32 elements (random "
-                         "data), for rocprofv3 kernel-trace and FETCH_SIZE/WRITE_SIZE summaries of the streams")
+                    help="only run each of the eight elementwise ops over 2^LOG2N fp32 elements (random data), "
+                         "rotating over SETS operand sets, for rocprofv3 kernel-trace and FETCH_SIZE/WRITE_SIZE "
+                         "summaries of the streams")
+    ap.add_argument("--log2n", type=int, default=28, help="--elementwise-profile: elements per operand (2^LOG2N)")
+    ap.add_argument("--sets", type=int, default=1, help="--elementwise-profile: operand sets rotated over")
+    ap.add_argument("--gemm-compare", action="store_true",
+                    help="only run the bf16 forward GEMM (c3hip_linear_fwd, bias + ReLU) and torch.matmul "
+                         "(hipBLASLt) alternately at 8192x4096x4096 and 16384x8192x8192 on random data, for "
+                         "rocprofv3 kernel-trace and MFMA-busy/clock counter summaries of both")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain copy-like stream (scale: read 2^26 fp32, write 2^26 fp32) three times; "
                          "its FETCH_SIZE/WRITE_SIZE counters calibrate the HBM traffic figures")
@@ -70,23 +77,75 @@ def copy_calibration():
                                            "write_bytes": 4 * n, "launches": 3}}), flush=True)
 
 
-def elementwise_profile(n=1 << 28, reps=3):
+def elementwise_profile(log2n=28, sets=1, reps=3):
+    """Each elementwise op `reps` times per operand set, rotating over `sets`
+    sets (sets > 1 keeps each launch's operands out of the Infinity Cache)."""
     import torch
 
     from c3_amd import native as C
 
     C.init(0)
+    n = 1 << log2n
     g = torch.Generator(device="cuda:0")
     g.manual_seed(0xE7)
-    a = torch.randn(n, device="cuda:0", generator=g)
-    b = torch.rand(n, device="cuda:0", generator=g) * 1.5 + 0.5
-    o = torch.empty(n, device="cuda:0")
+    bufs = [(torch.randn(n, device="cuda:0", generator=g), torch.rand(n, device="cuda:0", generator=g) * 1.5 + 0.5,
+             torch.empty(n, device="cuda:0")) for _ in range(sets)]
     s = torch.cuda.current_stream().cuda_stream
     for name, code in C.EW_OPS.items():
         for _ in range(reps):
-            C.elementwise(code, C.F32, a.data_ptr(), b.data_ptr(), 0.5, o.data_ptr(), n, 0, s)
+            for a, b, o in bufs:
+                C.elementwise(code, C.F32, a.data_ptr(), b.data_ptr(), 0.5, o.data_ptr(), n, 0, s)
     torch.cuda.synchronize()
-    print(json.dumps({"elementwise_profile": {"n": n, "launches_per_op": reps, "ops": list(C.EW_OPS)}}), flush=True)
+    print(json.dumps({"elementwise_profile": {"n": n, "operand_sets": sets, "launches_per_op": reps * sets,
+                                              "ops": list(C.EW_OPS)}}), flush=True)
+
+
+def gemm_compare(reps=10, rounds=3):
+    """bf16 forward GEMM of this backend (c3hip_linear_fwd with bias and ReLU)
+    against torch.matmul (hipBLASLt's kernel; no bias) on the same random
+    operands, alternating in rounds so both see the same clock and power
+    state.  Prints the event-timed TFLOP/s of each; the kernel durations,
+    MFMA busy and clock come from rocprofv3 over this same command."""
+    import torch
+
+    from c3_amd import native as C
+
+    C.init(0)
+    dev = torch.device("cuda:0")
+    s = torch.cuda.current_stream().cuda_stream
+    g = torch.Generator(device=dev)
+    g.manual_seed(0xB1A5)
+    out = {}
+    for (m, k, n) in [(8192, 4096, 4096), (16384, 8192, 8192)]:
+        X = torch.randn(m, k, device=dev, generator=g).to(torch.bfloat16)
+        W = (torch.randn(k, n, device=dev, generator=g) / float(k) ** 0.5).to(torch.bfloat16)
+        b = torch.randn(n, device=dev, generator=g) * 0.1
+        Y = torch.empty(m, n, device=dev, dtype=torch.bfloat16)
+        Yt = torch.empty(m, n, device=dev, dtype=torch.bfloat16)
+
+        def ours():
+            C.linear_fwd(C.BF16, X.data_ptr(), W.data_ptr(), b.data_ptr(), Y.data_ptr(), m, k, n, C.ACT_RELU, s)
+
+        def theirs():
+            torch.matmul(X, W, out=Yt)
+
+        times = {"c3hip_linear_fwd": [], "torch.matmul (hipBLASLt)": []}
+        for _ in range(rounds):
+            for name, fn in (("c3hip_linear_fwd", ours), ("torch.matmul (hipBLASLt)", theirs)):
+                fn()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                torch.cuda.synchronize()
+                e0.record()
+                for _ in range(reps):
+                    fn()
+                e1.record()
+                torch.cuda.synchronize()
+                times[name].append(e0.elapsed_time(e1) / reps)
+        out[f"{m}x{k}x{n}"] = {name: round(2.0 * m * n * k / (sorted(v)[len(v) // 2] * 1e-3) / 1e12, 1)
+                               for name, v in times.items()}
+        del X, W, b, Y, Yt
+        torch.cuda.empty_cache()
+    print(json.dumps({"gemm_compare_tflops": out, "launches_per_kernel_and_shape": rounds * (reps + 1)}), flush=True)
 
 
 def main():
@@ -99,7 +158,10 @@ def main():
         copy_calibration()
         return
     if args.elementwise_profile:
-        elementwise_profile()
+        elementwise_profile(args.log2n, args.sets)
+        return
+    if args.gemm_compare:
+        gemm_compare()
         return
 
     import torch
