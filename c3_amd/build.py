@@ -61,9 +61,15 @@ def build_runtime() -> Path:
     out = LIB / "libc3hip.so"
     srcs = [str(CSRC / s) for s in RUNTIME_SOURCES]
     # Host-only C++: no device code in these files, so hipcc only supplies the
-    # HIP headers and links libamdhip64.
+    # HIP headers and links libamdhip64.  c3hip_noalloc.hip holds a static
+    # device array (the no-alloc entry point's scratch), so it is compiled as
+    # HIP for gfx950 and its fat binary is linked into the library.
+    noalloc_obj = LIB / "c3hip_noalloc.o"
+    _run([HIPCC, "-x", "hip", f"--offload-arch={ARCH}", "-O2", "-std=c++17", "-fPIC", "-c", "-Wall",
+          *NO_PACKED_FP32, f"-I{INCLUDE}", f"-I{CSRC / 'runtime'}", str(CSRC / "runtime" / "c3hip_noalloc.hip"),
+          "-o", str(noalloc_obj)])
     cmd = [HIPCC, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", f"-I{INCLUDE}", f"-I{CSRC / 'runtime'}",
-           *srcs, "-o", str(out), "-ldl"]
+           *srcs, "-x", "none", str(noalloc_obj), f"--offload-arch={ARCH}", "-o", str(out), "-ldl"]
     _run(cmd)
     return out
 

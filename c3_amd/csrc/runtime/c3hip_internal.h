@@ -88,4 +88,24 @@ struct ChainArgs {
 
 inline bool aligned16(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Device workspace given to a GEMM plan.  base == nullptr: the plan takes its
+// workspace from the stream-ordered pool (hipMallocAsync / hipFreeAsync);
+// otherwise it uses [base, base + bytes) and fails with C3HIP_ERR_TOO_LARGE,
+// before launching anything, when it needs more.
+struct Workspace {
+    void* base = nullptr;
+    size_t bytes = 0;
+};
+
+// Fused Linear forward (c3hip_linear_fwd) with its workspace from ws (NULL:
+// the stream-ordered pool).  With a caller workspace it never takes the
+// transposed-W forward, which needs a second workspace (same bits either way).
+int linear_fwd(int dtype, const void* X, const void* W, const float* b, void* Y, int64_t M, int64_t K, int64_t N,
+               int act, hipStream_t stream, const Workspace* ws);
+
+// Set-up of the static scratch of c3hip_linear_fwd_noalloc on `device` (the
+// current device): records its device address.  Called by c3hip_init and by
+// the entry point's first call on a device.
+int noalloc_setup(int device);
+
 }  // namespace c3hip

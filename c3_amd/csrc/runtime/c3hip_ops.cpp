@@ -204,11 +204,38 @@ const Tile* choose_bf16_direct(Kind kind, const GemmArgs& a, bool* unsupported, 
     return nullptr;
 }
 
+// A workspace of `bytes` for one call: from ws when it has a base (capacity
+// checked, nothing launched on failure), else from the stream-ordered pool;
+// *owned tells release_workspace to free it.
+int take_workspace(const Workspace* ws, size_t bytes, hipStream_t stream, void** p, bool* owned, const char* what) {
+    *owned = false;
+    if (ws && ws->base) {
+        if (bytes > ws->bytes)
+            return set_error(C3HIP_ERR_TOO_LARGE, std::string(what) + " needs " + std::to_string(bytes) +
+                                                      " bytes of workspace, more than the " + std::to_string(ws->bytes) +
+                                                      " bytes given");
+        *p = ws->base;
+        return C3HIP_OK;
+    }
+    hipError_t e = hipMallocAsync(p, bytes, stream);
+    if (e != hipSuccess) return set_error(C3HIP_ERR_HIP, std::string("hipMallocAsync(") + what + "): " + hipGetErrorString(e));
+    *owned = true;
+    return C3HIP_OK;
+}
+
+int release_workspace(void* p, bool owned, int rc, hipStream_t stream, const char* what) {
+    if (!owned) return rc;
+    hipError_t e = hipFreeAsync(p, stream);
+    if (rc == C3HIP_OK && e != hipSuccess)
+        rc = set_error(C3HIP_ERR_HIP, std::string("hipFreeAsync(") + what + "): " + hipGetErrorString(e));
+    return rc;
+}
+
 // Split-K run of a plain bf16 GEMM on direct tile d: S block rows write fp32
 // partial products into a stream-ordered workspace [S, M, N]; the reduction
 // adds them in split order and applies the kind's epilogue (forward: bias and
 // activation, bf16 out; dW: fp32 out; the others: bf16 out).
-int run_split(Kind kind, const GemmArgs& a0, const Tile* d, int S, hipStream_t stream) {
+int run_split(Kind kind, const GemmArgs& a0, const Tile* d, int S, hipStream_t stream, const Workspace* wsp) {
     // fp32-output kernel of the same operand layouts (FwdT: both k-contiguous, as dX).
     const char* kn = kind == Kind::Fwd                          ? "fwdf"
                      : (kind == Kind::Dx || kind == Kind::FwdT) ? "dxf"
@@ -216,9 +243,10 @@ int run_split(Kind kind, const GemmArgs& a0, const Tile* d, int S, hipStream_t s
                                                                 : "dw";
     const bool fwd = kind == Kind::Fwd || kind == Kind::FwdT;
     float* ws = nullptr;
+    bool owned = false;
     const int64_t slice = a0.M * a0.N;
-    hipError_t e = hipMallocAsync((void**)&ws, (size_t)S * (size_t)slice * sizeof(float), stream);
-    if (e != hipSuccess) return set_error(C3HIP_ERR_HIP, std::string("hipMallocAsync(split-K): ") + hipGetErrorString(e));
+    int rc = take_workspace(wsp, (size_t)S * (size_t)slice * sizeof(float), stream, (void**)&ws, &owned, "split-K");
+    if (rc) return rc;
     GemmArgs g = a0;
     g.C = ws;
     g.ldc = a0.N;
@@ -230,7 +258,7 @@ int run_split(Kind kind, const GemmArgs& a0, const Tile* d, int S, hipStream_t s
     std::snprintf(name, sizeof(name), "c3_gemm_bf16_%s_%s", kn, d->name);
     const int64_t tiles = tile_count(a0, d);
     void* args[] = {&g};
-    int rc = launch(name, dim3((unsigned)tiles, (unsigned)S), dim3(d->threads), args, stream);
+    rc = launch(name, dim3((unsigned)tiles, (unsigned)S), dim3(d->threads), args, stream);
     if (rc == C3HIP_OK) {
         SplitReduceArgs r{};
         r.ws = ws;
@@ -247,10 +275,7 @@ int run_split(Kind kind, const GemmArgs& a0, const Tile* d, int S, hipStream_t s
         void* rargs[] = {&r};
         rc = launch("c3_splitk_reduce", dim3((unsigned)((threads + 255) / 256)), dim3(256), rargs, stream);
     }
-    e = hipFreeAsync(ws, stream);
-    if (rc == C3HIP_OK && e != hipSuccess)
-        rc = set_error(C3HIP_ERR_HIP, std::string("hipFreeAsync(split-K): ") + hipGetErrorString(e));
-    return rc;
+    return release_workspace(ws, owned, rc, stream, "split-K");
 }
 
 // bf16 kernels always move 16-byte vectors (8 elements): the contiguous
@@ -283,13 +308,15 @@ int plan_split_f32(const GemmArgs& a, const Tile* t) {
     return S >= 2 ? (int)S : 0;
 }
 
-int run_split_f32(Kind kind, const GemmArgs& a0, const Tile* t, int S, bool vec, hipStream_t stream) {
+int run_split_f32(Kind kind, const GemmArgs& a0, const Tile* t, int S, bool vec, hipStream_t stream,
+                  const Workspace* wsp) {
     const int64_t split_k = ((a0.K + S - 1) / S + 15) / 16 * 16;
     S = (int)((a0.K + split_k - 1) / split_k);
     const int64_t slice = a0.M * a0.N;
     float* ws = nullptr;
-    hipError_t e = hipMallocAsync((void**)&ws, (size_t)S * (size_t)slice * sizeof(float), stream);
-    if (e != hipSuccess) return set_error(C3HIP_ERR_HIP, std::string("hipMallocAsync(split-K): ") + hipGetErrorString(e));
+    bool owned = false;
+    int rc = take_workspace(wsp, (size_t)S * (size_t)slice * sizeof(float), stream, (void**)&ws, &owned, "split-K");
+    if (rc) return rc;
     GemmArgs g = a0;
     g.C = ws;
     g.ldc = a0.N;
@@ -300,7 +327,7 @@ int run_split_f32(Kind kind, const GemmArgs& a0, const Tile* t, int S, bool vec,
     char name[96];
     std::snprintf(name, sizeof(name), "c3_gemm_f32_%s_%s_%s", kind_name(kind), t->name, vec ? "v" : "s");
     void* args[] = {&g};
-    int rc = launch(name, dim3((unsigned)tile_count(a0, t), (unsigned)S), dim3(t->threads), args, stream);
+    rc = launch(name, dim3((unsigned)tile_count(a0, t), (unsigned)S), dim3(t->threads), args, stream);
     if (rc == C3HIP_OK) {
         SplitReduceArgs r{};
         r.ws = ws;
@@ -317,13 +344,11 @@ int run_split_f32(Kind kind, const GemmArgs& a0, const Tile* t, int S, bool vec,
         void* rargs[] = {&r};
         rc = launch("c3_splitk_reduce", dim3((unsigned)((threads + 255) / 256)), dim3(256), rargs, stream);
     }
-    e = hipFreeAsync(ws, stream);
-    if (rc == C3HIP_OK && e != hipSuccess)
-        rc = set_error(C3HIP_ERR_HIP, std::string("hipFreeAsync(split-K): ") + hipGetErrorString(e));
-    return rc;
+    return release_workspace(ws, owned, rc, stream, "split-K");
 }
 
-int run_gemm(int dtype, Kind kind, const GemmArgs& a0, bool a_kc, bool b_kc, hipStream_t stream) {
+int run_gemm(int dtype, Kind kind, const GemmArgs& a0, bool a_kc, bool b_kc, hipStream_t stream,
+             const Workspace* ws = nullptr) {
     GemmArgs a = a0;
     if (a.M == 0 || a.N == 0) return C3HIP_OK;
     if (dtype == C3HIP_BF16) {
@@ -337,7 +362,7 @@ int run_gemm(int dtype, Kind kind, const GemmArgs& a0, bool a_kc, bool b_kc, hip
             return set_error(C3HIP_ERR_UNSUPPORTED, std::string("tile ") + t_tile_bf16 +
                                                         " cannot run this GEMM (masked operand, db side output, "
                                                         "K not a multiple of its k depth, or M or N below 8)");
-        if (d && split > 1) return run_split(kind, a, d, split, stream);
+        if (d && split > 1) return run_split(kind, a, d, split, stream, ws);
         if (!d && kind == Kind::FwdT) return set_error(C3HIP_ERR_UNSUPPORTED, "transposed-W forward needs a direct tile");
         if (d) {
             char name[96];
@@ -356,7 +381,7 @@ int run_gemm(int dtype, Kind kind, const GemmArgs& a0, bool a_kc, bool b_kc, hip
     }
     const Tile* t = choose_f32_tile(kind, a.M, a.N);
     const bool vec = vec_ok(a_kc, a.M, a.K, a.lda, a.A, a.Amask) && vec_ok(b_kc, a.N, a.K, a.ldb, a.B, a.Bmask);
-    if (const int S = plan_split_f32(a, t)) return run_split_f32(kind, a, t, S, vec, stream);
+    if (const int S = plan_split_f32(a, t)) return run_split_f32(kind, a, t, S, vec, stream, ws);
     char name[96];
     std::snprintf(name, sizeof(name), "c3_gemm_f32_%s_%s_%s", kind_name(kind), t->name, vec ? "v" : "s");
     const int64_t blocks = ((a.M + t->bm - 1) / t->bm) * ((a.N + t->bn - 1) / t->bn);
@@ -534,6 +559,24 @@ int linear_bwd_prepass(int dtype, const void* X, const void* W, const void* Y, c
 }
 
 }  // namespace
+
+int linear_fwd(int dtype, const void* X, const void* W, const float* b, void* Y, int64_t M, int64_t K, int64_t N,
+               int act, hipStream_t stream, const Workspace* ws) {
+    int rc = check_dtype(dtype);
+    if (rc) return rc;
+    if (act < C3HIP_ACT_NONE || act > C3HIP_ACT_TANH) return set_error(C3HIP_ERR_INVALID, "unknown act");
+    if ((rc = check_elems("X", M, K)) || (rc = check_elems("W", K, N)) || (rc = check_elems("Y", M, N))) return rc;
+    if (M > 0 && N > 0 && (!Y || (K > 0 && (!X || !W)))) return set_error(C3HIP_ERR_INVALID, "null pointer");
+    GemmArgs a{};
+    a.A = X; a.B = W; a.C = Y; a.bias = b;
+    a.M = M; a.N = N; a.K = K;
+    a.lda = K; a.ldb = N; a.ldc = N;
+    a.act = act;
+    if (!(ws && ws->base) && dtype == C3HIP_BF16 && M > 0 && N > 0 && K > 0 && bf16_fwd_transposed(a))
+        return linear_fwd_wt(a, stream);
+    return run_gemm(dtype, Kind::Fwd, a, true, false, stream, ws);
+}
+
 }  // namespace c3hip
 
 using namespace c3hip;
@@ -688,18 +731,7 @@ int c3hip_matmul(int dtype, const void* A, const void* B, void* C, int64_t M, in
 int c3hip_linear_fwd(int dtype, const void* X, const void* W, const float* b, void* Y, int64_t M, int64_t K,
                      int64_t N, int act, void* stream) {
     clear_error();
-    int rc = check_dtype(dtype);
-    if (rc) return rc;
-    if (act < C3HIP_ACT_NONE || act > C3HIP_ACT_TANH) return set_error(C3HIP_ERR_INVALID, "unknown act");
-    if ((rc = check_elems("X", M, K)) || (rc = check_elems("W", K, N)) || (rc = check_elems("Y", M, N))) return rc;
-    if (M > 0 && N > 0 && (!Y || (K > 0 && (!X || !W)))) return set_error(C3HIP_ERR_INVALID, "null pointer");
-    GemmArgs a{};
-    a.A = X; a.B = W; a.C = Y; a.bias = b;
-    a.M = M; a.N = N; a.K = K;
-    a.lda = K; a.ldb = N; a.ldc = N;
-    a.act = act;
-    if (dtype == C3HIP_BF16 && M > 0 && N > 0 && K > 0 && bf16_fwd_transposed(a)) return linear_fwd_wt(a, (hipStream_t)stream);
-    return run_gemm(dtype, Kind::Fwd, a, true, false, (hipStream_t)stream);
+    return c3hip::linear_fwd(dtype, X, W, b, Y, M, K, N, act, (hipStream_t)stream, nullptr);
 }
 
 // Both GEMMs of a small fp32 layer backward in one launch (c3_gemm_f32_bwd*):

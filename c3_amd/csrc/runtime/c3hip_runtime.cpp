@@ -184,9 +184,17 @@ int init_device(int device) {
                                                 std::to_string(count) + ")");
     e = hipSetDevice(device);
     if (e != hipSuccess) return set_error(C3HIP_ERR_HIP, std::string("hipSetDevice failed: ") + hipGetErrorString(e));
-    std::lock_guard<std::mutex> lock(g_mu);
-    DeviceState* ds = nullptr;
-    return load_device(device, &ds);
+    {
+        std::lock_guard<std::mutex> lock(g_mu);
+        DeviceState* ds = nullptr;
+        const int rc = load_device(device, &ds);
+        if (rc) return rc;
+    }
+    // Set-up of c3hip_linear_fwd_noalloc's static scratch on this device.  A
+    // failure is kept and reported by that entry point; the other entry
+    // points do not depend on it.
+    if (noalloc_setup(device) != C3HIP_OK) clear_error();
+    return C3HIP_OK;
 }
 
 int load_code_object(const char* module_name, const void* image, size_t nbytes) {

@@ -52,6 +52,7 @@ SIGNATURES = {
                                     ctypes.POINTER(_vp), _i64, _vp]),
     "c3hip_matmul": (_int, [_int, _vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _vp]),
     "c3hip_linear_fwd": (_int, [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _vp]),
+    "c3hip_linear_fwd_noalloc": (_int, [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _vp]),
     "c3hip_linear_bwd": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _vp]),
     "c3hip_sum_reduce": (_int, [_vp, _vp, _i64, _i64, _int, _vp]),
     "c3hip_softmax_ce": (_int, [_int, _vp, _vp, _vp, _vp, _i64, _i64, _vp]),
@@ -152,6 +153,16 @@ def matmul(dtype: int, A: int, B: int, C: int, M: int, K: int, N: int, transA: b
 def linear_fwd(dtype: int, X: int, W: int, b: int | None, Y: int, M: int, K: int, N: int, act: int = ACT_RELU,
                stream: int = 0) -> None:
     _check("c3hip_linear_fwd", load().c3hip_linear_fwd(dtype, X, W, b, Y, M, K, N, act, stream))
+
+
+# Bytes of c3hip_linear_fwd_noalloc's per-device static scratch (C3HIP_NOALLOC_SCRATCH_BYTES).
+NOALLOC_SCRATCH_BYTES = 32 << 20
+
+
+def linear_fwd_noalloc(dtype: int, X: int, W: int, b: int | None, Y: int, M: int, K: int, N: int,
+                       act: int = ACT_RELU, stream: int = 0) -> None:
+    """c3hip_linear_fwd with its workspace in the library's static scratch (no allocation)."""
+    _check("c3hip_linear_fwd_noalloc", load().c3hip_linear_fwd_noalloc(dtype, X, W, b, Y, M, K, N, act, stream))
 
 
 def linear_bwd(dtype: int, X: int | None, W: int | None, Y: int | None, dY: int, dX: int | None, dW: int | None,

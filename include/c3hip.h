@@ -202,6 +202,29 @@ int c3hip_matmul(int dtype, const void* A, const void* B, void* C, int64_t M, in
 int c3hip_linear_fwd(int dtype, const void* X, const void* W, const float* b, void* Y, int64_t M,
                      int64_t K, int64_t N, int act, void* stream);
 
+/* Bytes of the per-device static scratch of c3hip_linear_fwd_noalloc. */
+#define C3HIP_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+/*
+ * c3hip_linear_fwd that allocates no device memory: same arguments, kernels,
+ * launch plan and results (bit for bit) as c3hip_linear_fwd, with its only
+ * workspace (the fp32 split-K partials of a grid too small to fill the chip)
+ * in a static per-device array of C3HIP_NOALLOC_SCRATCH_BYTES (32 MiB),
+ * which each device that runs it holds until the process ends.  Every
+ * forward the size heuristic plans fits; a larger need (only possible with a
+ * tile forced by c3hip_set_gemm_tile) fails with C3HIP_ERR_TOO_LARGE before
+ * anything is launched.  Call c3hip_init(device) first: it loads the code
+ * objects and looks up the scratch, so the entry point itself calls no
+ * hipMalloc / hipFree.  Calls on one device share the scratch: calls whose
+ * work overlaps in time on that device (different streams or host threads)
+ * race; calls on one stream are ordered and safe.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation).
+ */
+int c3hip_linear_fwd_noalloc(int dtype, const void* X, const void* W, const float* b, void* Y, int64_t M,
+                             int64_t K, int64_t N, int act, void* stream);
+
 /*
  * Fused Linear backward.  With dZ = (Y > 0 ? 1 : 0) * dY when act ==
  * C3HIP_ACT_RELU, dY * (Y * (1 - Y)) for C3HIP_ACT_SIGMOID, dY * (1 - Y * Y)
