@@ -36,33 +36,46 @@ const char* kindName(KernelKind k) {
 }
 
 // The default backend: resolve the spec's code object through the JIT cache
-// (cached image if present, else the prebuilt file, which is then cached)
-// and wrap the spec in a HipCompiledKernel.
+// and wrap the spec in a HipCompiledKernel.  The authoritative image is the
+// prebuilt code object the library ships beside itself; a cache entry is used
+// only when it holds that same image (same SHA-256; entries from another
+// build or with a damaged object are evicted by the lookup), otherwise the
+// prebuilt image is read and cached.  Either way the image is handed to
+// c3hip_load_code_object, which loads it or, when the module is already
+// loaded on the device, checks that it is the loaded image.
 std::shared_ptr<CompiledKernel> hipFactory(const KernelSpec& spec, const CompileOptions& opts, std::string* err) {
     const std::string spec_str = spec.toString();
     const std::string key = JITCache::makeKey(spec_str, opts.opt_level);
     const std::string module = spec.moduleName();
     if (!module.empty() && opts.use_cache && JITCache::isEnabled()) {
         JITCache& cache = JITCache::getInstance();
+        char path[4096];
+        if (c3hip_code_object_path(module.c_str(), path, sizeof(path)) != C3HIP_OK) {
+            *err = "no code object path for module " + module;
+            return nullptr;
+        }
+        const std::string prebuilt_sha = cache.fileSha(path);
+        if (prebuilt_sha.empty()) {
+            *err = std::string("prebuilt code object ") + path + " not found";
+            return nullptr;
+        }
         std::vector<char> image;
-        const std::string hit = cache.lookup(key);
+        const std::string hit = cache.lookup(key, prebuilt_sha);
         if (!hit.empty()) {
             if (!JITCache::readFile(hit, &image) || image.empty()) {
                 *err = "JITCache: cannot read " + hit;
                 return nullptr;
             }
-            if (c3hip_load_code_object(module.c_str(), image.data(), image.size()) != C3HIP_OK) {
-                *err = std::string("loading cached code object failed: ") + c3hip_last_error();
-                return nullptr;
-            }
         } else {
-            char path[4096];
-            if (c3hip_code_object_path(module.c_str(), path, sizeof(path)) != C3HIP_OK ||
-                !JITCache::readFile(path, &image) || image.empty()) {
-                *err = "prebuilt code object for module " + module + " not found";
+            if (!JITCache::readFile(path, &image) || image.empty()) {
+                *err = std::string("cannot read prebuilt code object ") + path;
                 return nullptr;
             }
             (void)cache.store(key, image, {"module=" + module, "spec=" + spec_str});
+        }
+        if (c3hip_load_code_object(module.c_str(), image.data(), image.size()) != C3HIP_OK) {
+            *err = std::string("loading code object failed: ") + c3hip_last_error();
+            return nullptr;
         }
     }
     return std::make_shared<HipCompiledKernel>(spec, opts.opt_level, key);

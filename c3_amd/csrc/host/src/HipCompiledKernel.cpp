@@ -8,6 +8,8 @@
 // reference) from the device caching pool, and no host copies are made.
 #include "C3/HipCompiledKernel.h"
 
+#include <initializer_list>
+
 #include <stdexcept>
 
 #include "c3hip.h"
@@ -71,6 +73,18 @@ std::vector<Tensor> HipCompiledKernel::execute(const std::vector<Tensor>& in) {
                                              shapeToString(s.input_shapes[i]));
         }
     };
+    // GEMM kinds read every operand with the spec's element type (registry
+    // keys do not carry the dtype, so a kernel can be reached with other
+    // operands): a mismatch throws, and the registry falls back to eager.
+    auto sameDtype = [&](std::initializer_list<size_t> idx, const char* what) {
+        for (size_t i : idx) {
+            if (in[i].dtype() != s.dtype)
+                throw std::runtime_error(std::string(what) + ": input " + std::to_string(i) + " is " +
+                                         (in[i].dtype() == DType::kBFloat16 ? "bf16" : "fp32") + ", kernel compiled for " +
+                                         (s.dtype == DType::kBFloat16 ? "bf16" : "fp32"));
+            if (in[i].shape().size() != 2) throw std::runtime_error(std::string(what) + ": operands must be 2-D");
+        }
+    };
     void* st = t_stream;
     TileGuard tile_guard(s);
     switch (s.kind) {
@@ -103,8 +117,8 @@ std::vector<Tensor> HipCompiledKernel::execute(const std::vector<Tensor>& in) {
         }
         case KernelKind::MatMul: {
             need(2);
+            sameDtype({0, 1}, "matmul");
             const Tensor &A = in[0], &B = in[1];
-            if (A.shape().size() != 2 || B.shape().size() != 2) throw std::runtime_error("matmul takes 2-D operands");
             const size_t M = s.transA ? A.shape()[1] : A.shape()[0], K = s.transA ? A.shape()[0] : A.shape()[1];
             const size_t KB = s.transB ? B.shape()[1] : B.shape()[0], N = s.transB ? B.shape()[0] : B.shape()[1];
             if (K != KB) throw std::runtime_error("matmul: inner dimensions differ");
@@ -118,6 +132,7 @@ std::vector<Tensor> HipCompiledKernel::execute(const std::vector<Tensor>& in) {
             // [X, W, b] for MatMul+Add+act, [X, W] for MatMul+act.
             const bool has_bias = s.input_shapes.size() != 2;
             need(has_bias ? 3 : 2);
+            sameDtype({0, 1}, "linear");
             const Tensor &X = in[0], &W = in[1];
             const size_t M = X.shape()[0], K = X.shape()[1], N = W.shape()[1];
             if (W.shape()[0] != K || (has_bias && (in[2].numel() != N || in[2].dtype() != DType::kFloat)))
@@ -177,6 +192,7 @@ std::vector<Tensor> HipCompiledKernel::execute(const std::vector<Tensor>& in) {
         }
         case KernelKind::MatMulBackwardA: {
             need(2);  // [grad(M,N), B(K,N)] -> grad . B^T (M,K)
+            sameDtype({0, 1}, "matmul backward A");
             const Tensor &g = in[0], &B = in[1];
             const size_t M = g.shape()[0], N = g.shape()[1], K = B.shape()[0];
             if (B.shape()[1] != N) throw std::runtime_error("matmul backward A: shapes do not agree");
@@ -188,6 +204,7 @@ std::vector<Tensor> HipCompiledKernel::execute(const std::vector<Tensor>& in) {
         }
         case KernelKind::MatMulBackwardB: {
             need(2);  // [grad(M,N), A(M,K)] -> A^T . grad (K,N)
+            sameDtype({0, 1}, "matmul backward B");
             const Tensor &g = in[0], &A = in[1];
             const size_t M = g.shape()[0], N = g.shape()[1], K = A.shape()[1];
             if (A.shape()[0] != M) throw std::runtime_error("matmul backward B: shapes do not agree");
@@ -199,8 +216,11 @@ std::vector<Tensor> HipCompiledKernel::execute(const std::vector<Tensor>& in) {
         }
         case KernelKind::LinearBwd: {
             need(4);  // [dY, X, W, Y] -> [dX, dW, db]; dX empty when the spec asks for no input gradient
+            sameDtype({0, 1, 2, 3}, "linear backward");
             const Tensor &dY = in[0], &X = in[1], &W = in[2], &Y = in[3];
             const size_t M = X.shape()[0], K = X.shape()[1], N = W.shape()[1];
+            if (W.shape()[0] != K || dY.shape() != std::vector<size_t>{M, N} || Y.shape() != dY.shape())
+                throw std::runtime_error("linear backward: shapes of dY, X, W, Y do not agree");
             Tensor dX = s.input_grad ? Tensor(ShapeTag{}, {M, K}, X.dtype(), DeviceType::kHIP) : Tensor();
             Tensor dW(ShapeTag{}, {K, N}, DType::kFloat, DeviceType::kHIP);
             Tensor db(ShapeTag{}, {N}, DType::kFloat, DeviceType::kHIP);

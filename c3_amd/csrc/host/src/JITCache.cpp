@@ -2,6 +2,7 @@
 #include "C3/JITCache.h"
 
 #include <dirent.h>
+#include <errno.h>
 #include <sys/stat.h>
 #include <unistd.h>
 
@@ -60,14 +61,13 @@ bool ensureDir(const std::string& dir) {
 
 }  // namespace
 
-std::string sha256_hex(const std::string& data) {
+std::string sha256_hex(const char* data, size_t n) {
     uint32_t h[8] = {0x6a09e667, 0xbb67ae85, 0x3c6ef372, 0xa54ff53a, 0x510e527f, 0x9b05688c, 0x1f83d9ab, 0x5be0cd19};
-    const size_t n = data.size();
     size_t i = 0;
-    for (; i + 64 <= n; i += 64) compress(h, reinterpret_cast<const unsigned char*>(data.data()) + i);
+    for (; i + 64 <= n; i += 64) compress(h, reinterpret_cast<const unsigned char*>(data) + i);
     unsigned char tail[128] = {0};
     const size_t rem = n - i;
-    std::memcpy(tail, data.data() + i, rem);
+    if (rem) std::memcpy(tail, data + i, rem);
     tail[rem] = 0x80;
     const size_t tail_len = rem + 1 + 8 <= 64 ? 64 : 128;
     const uint64_t bits = (uint64_t)n * 8;
@@ -78,6 +78,8 @@ std::string sha256_hex(const std::string& data) {
     for (int b = 0; b < 8; ++b) std::snprintf(out + 8 * b, 9, "%08x", h[b]);
     return std::string(out, 64);
 }
+
+std::string sha256_hex(const std::string& data) { return sha256_hex(data.data(), data.size()); }
 
 JITCache& JITCache::getInstance() {
     static JITCache c;
@@ -106,20 +108,87 @@ std::string JITCache::resolveCacheDir() {
 
 std::string JITCache::cacheDir() const { return resolveCacheDir(); }
 
-std::string JITCache::lookup(const std::string& key) {
+namespace {
+
+std::string objectPath(const std::string& dir, const std::string& sha) { return dir + "/c3_jit_obj_" + sha + ".hsaco"; }
+std::string metaPath(const std::string& dir, const std::string& key) { return dir + "/c3_jit_" + key + ".meta"; }
+
+// Write `n` bytes to `path` through a temporary file renamed into place.
+bool writeAtomically(const std::string& path, const char* data, size_t n) {
+    const std::string tmp = path + ".tmp" + std::to_string(getpid());
+    {
+        std::ofstream o(tmp, std::ios::binary);
+        if (!o.is_open()) return false;
+        o.write(data, (std::streamsize)n);
+        if (!o.good()) {
+            o.close();
+            unlink(tmp.c_str());
+            return false;
+        }
+    }
+    if (rename(tmp.c_str(), path.c_str()) != 0) {
+        unlink(tmp.c_str());
+        return false;
+    }
+    return true;
+}
+
+}  // namespace
+
+// SHA-256 (hex) of the file's current bytes, "" when it cannot be read.
+static std::string hashFile(const std::string& path) {
+    std::vector<char> bytes;
+    if (!JITCache::readFile(path, &bytes)) return "";
+    return sha256_hex(bytes.data(), bytes.size());
+}
+
+std::string JITCache::fileShaLocked(const std::string& path) {
+    struct stat st;
+    if (stat(path.c_str(), &st) != 0) return "";
+    const int64_t mt = (int64_t)st.st_mtim.tv_sec * 1000000000LL + st.st_mtim.tv_nsec;
+    auto it = sha_memo_.find(path);
+    if (it != sha_memo_.end() && it->second.size == (int64_t)st.st_size && it->second.mtime_ns == mt)
+        return it->second.sha;
+    std::vector<char> bytes;
+    if (!readFile(path, &bytes)) return "";
+    FileStamp fs;
+    fs.size = (int64_t)st.st_size;
+    fs.mtime_ns = mt;
+    fs.sha = sha256_hex(bytes.data(), bytes.size());
+    sha_memo_[path] = fs;
+    return fs.sha;
+}
+
+std::string JITCache::fileSha(const std::string& path) {
+    std::lock_guard<std::mutex> lk(mutex_);
+    return fileShaLocked(path);
+}
+
+std::string JITCache::lookup(const std::string& key, const std::string& expected_sha) {
     std::lock_guard<std::mutex> lk(mutex_);
     const std::string dir = resolveCacheDir();
-    const std::string obj = dir + "/c3_jit_" + key + ".hsaco";
-    const std::string meta = dir + "/c3_jit_" + key + ".meta";
-    if (access(obj.c_str(), R_OK) != 0) {
+    const std::string meta = metaPath(dir, key);
+    std::ifstream m(meta);
+    if (!m.is_open()) {
         misses_++;
         return "";
     }
-    std::ifstream m(meta);
-    std::string version;
-    if (!m.is_open() || !std::getline(m, version) || version != currentJITVersion()) {
-        unlink(obj.c_str());
+    std::string version, line, sha;
+    const bool versioned = std::getline(m, version) && version == currentJITVersion();
+    while (versioned && std::getline(m, line))
+        if (line.rfind("image=", 0) == 0) sha = line.substr(6);
+    m.close();
+    const std::string obj = sha.empty() ? "" : objectPath(dir, sha);
+    // The object is hashed in full on every lookup: a rewrite within the
+    // file system's timestamp granularity would fool a size/mtime memo.
+    const std::string obj_sha = obj.empty() || access(obj.c_str(), R_OK) != 0 ? "" : hashFile(obj);
+    const bool ok = versioned && !sha.empty() && obj_sha == sha && (expected_sha.empty() || sha == expected_sha);
+    if (!ok) {
+        // Stale version, missing or damaged object, or built from other code:
+        // drop the entry; a damaged object goes too (its name is its hash).
         unlink(meta.c_str());
+        if (!obj_sha.empty() && obj_sha != sha) unlink(obj.c_str());
+        if (versioned) rejected_++;
         misses_++;
         return "";
     }
@@ -132,38 +201,14 @@ std::string JITCache::store(const std::string& key, const std::vector<char>& ima
     std::lock_guard<std::mutex> lk(mutex_);
     const std::string dir = resolveCacheDir();
     if (!ensureDir(dir)) return "";
-    const std::string obj = dir + "/c3_jit_" + key + ".hsaco";
-    const std::string meta = dir + "/c3_jit_" + key + ".meta";
-    const std::string suffix = ".tmp" + std::to_string(getpid());
-    const std::string tobj = obj + suffix, tmeta = meta + suffix;
-    {
-        std::ofstream o(tobj, std::ios::binary);
-        if (!o.is_open()) return "";
-        o.write(image.data(), (std::streamsize)image.size());
-        if (!o.good()) {
-            unlink(tobj.c_str());
-            return "";
-        }
-    }
-    {
-        std::ofstream m(tmeta);
-        if (!m.is_open()) {
-            unlink(tobj.c_str());
-            return "";
-        }
-        m << currentJITVersion() << "\n";
-        for (const auto& l : meta_lines) m << l << "\n";
-    }
-    if (rename(tobj.c_str(), obj.c_str()) != 0) {
-        unlink(tobj.c_str());
-        unlink(tmeta.c_str());
-        return "";
-    }
-    if (rename(tmeta.c_str(), meta.c_str()) != 0) {
-        unlink(obj.c_str());
-        unlink(tmeta.c_str());
-        return "";
-    }
+    const std::string sha = sha256_hex(image.data(), image.size());
+    const std::string obj = objectPath(dir, sha);
+    if (hashFile(obj) != sha && !writeAtomically(obj, image.data(), image.size())) return "";
+    std::ostringstream mt;
+    mt << currentJITVersion() << "\n" << "image=" << sha << "\n";
+    for (const auto& l : meta_lines) mt << l << "\n";
+    const std::string text = mt.str();
+    if (!writeAtomically(metaPath(dir, key), text.data(), text.size())) return "";
     stores_++;
     return obj;
 }
@@ -189,6 +234,7 @@ void JITCache::evict() {
         if (std::strncmp(e->d_name, "c3_jit_", 7) == 0) unlink((dir + "/" + e->d_name).c_str());
     }
     closedir(d);
+    sha_memo_.clear();
 }
 
 }  // namespace c3

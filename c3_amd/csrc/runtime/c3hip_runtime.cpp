@@ -1,7 +1,7 @@
 // c3hip_runtime.cpp -- host side of the C ABI in include/c3hip.h.
 //
 // Loads the prebuilt gfx950 code objects (elementwise.hsaco, gemm_f32.hsaco,
-// gemm_bf16.hsaco, reduce.hsaco) with hipModuleLoad, resolves kernels by
+// gemm_bf16.hsaco, reduce.hsaco, loss.hsaco) with hipModuleLoadData, resolves kernels by
 // name, validates arguments, picks the kernel variant (tile shape, vector or
 // scalar loads) and launches it with hipModuleLaunchKernel on the caller's
 // stream.  Device buffers are the caller's; nothing is copied host<->device.
@@ -34,9 +34,52 @@ struct DeviceState {
     int device = -1;
     std::vector<hipModule_t> modules;
     std::vector<std::string> module_names;
+    std::vector<uint64_t> module_hashes;  // image_hash() of each loaded image
+    std::vector<size_t> module_sizes;
     std::unordered_map<std::string, hipFunction_t> fns;
     bool dir_scanned = false;
 };
+
+// 64-bit FNV-1a over the image bytes: identifies which image a loaded module
+// came from, so that a second registration of a module can be checked.
+uint64_t image_hash(const void* data, size_t n) {
+    const unsigned char* p = static_cast<const unsigned char*>(data);
+    uint64_t h = 0xcbf29ce484222325ull;
+    for (size_t i = 0; i < n; ++i) {
+        h ^= p[i];
+        h *= 0x100000001b3ull;
+    }
+    return h;
+}
+
+bool read_file(const std::string& path, std::vector<char>* out) {
+    FILE* f = std::fopen(path.c_str(), "rb");
+    if (!f) return false;
+    bool ok = std::fseek(f, 0, SEEK_END) == 0;
+    const long n = ok ? std::ftell(f) : -1;
+    ok = ok && n > 0 && std::fseek(f, 0, SEEK_SET) == 0;
+    if (ok) {
+        out->resize((size_t)n);
+        ok = std::fread(out->data(), 1, (size_t)n, f) == (size_t)n;
+    }
+    std::fclose(f);
+    return ok;
+}
+
+// Load `image` as module `name` on the current device (the caller holds g_mu).
+int add_module(DeviceState* ds, const std::string& name, const void* image, size_t nbytes, const std::string& what) {
+    hipModule_t m = nullptr;
+    const hipError_t e = hipModuleLoadData(&m, image);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return set_error(C3HIP_ERR_HIP, "hipModuleLoadData(" + what + ") failed: " + hipGetErrorString(e));
+    }
+    ds->modules.push_back(m);
+    ds->module_names.push_back(name);
+    ds->module_hashes.push_back(image_hash(image, nbytes));
+    ds->module_sizes.push_back(nbytes);
+    return C3HIP_OK;
+}
 
 std::mutex g_mu;
 std::unordered_map<int, std::unique_ptr<DeviceState>> g_devices;
@@ -49,11 +92,13 @@ bool known_module(const std::string& name) {
     return false;
 }
 
-bool has_module(const DeviceState& ds, const std::string& name) {
-    for (const auto& n : ds.module_names)
-        if (n == name) return true;
-    return false;
+int module_index(const DeviceState& ds, const std::string& name) {
+    for (size_t i = 0; i < ds.module_names.size(); ++i)
+        if (ds.module_names[i] == name) return (int)i;
+    return -1;
 }
+
+bool has_module(const DeviceState& ds, const std::string& name) { return module_index(ds, name) >= 0; }
 
 std::string library_dir() {
     Dl_info info;
@@ -91,15 +136,10 @@ int load_device(int device, DeviceState** out) {
         for (const char* name : kModuleNames) {
             if (has_module(*ds, name)) continue;
             const std::string path = dir + "/" + name + ".hsaco";
-            hipModule_t m = nullptr;
-            hipError_t e = hipModuleLoad(&m, path.c_str());
-            if (e != hipSuccess) {
-                (void)hipGetLastError();
-                return set_error(e == hipErrorFileNotFound ? C3HIP_ERR_NOT_FOUND : C3HIP_ERR_HIP,
-                                 "hipModuleLoad(" + path + ") failed: " + hipGetErrorString(e));
-            }
-            ds->modules.push_back(m);
-            ds->module_names.push_back(name);
+            std::vector<char> image;
+            if (!read_file(path, &image)) return set_error(C3HIP_ERR_NOT_FOUND, "cannot read code object " + path);
+            const int rc = add_module(ds, name, image.data(), image.size(), path);
+            if (rc) return rc;
         }
         ds->dir_scanned = true;
         // Workspaces (split-K partials, backward pre-pass buffers) come from
@@ -205,17 +245,16 @@ int load_code_object(const char* module_name, const void* image, size_t nbytes) 
     if (rc) return rc;
     std::lock_guard<std::mutex> lock(g_mu);
     DeviceState* ds = device_state(dev);
-    if (has_module(*ds, module_name)) return C3HIP_OK;
-    hipModule_t m = nullptr;
-    hipError_t e = hipModuleLoadData(&m, image);
-    if (e != hipSuccess) {
-        (void)hipGetLastError();
-        return set_error(C3HIP_ERR_HIP, std::string("hipModuleLoadData(") + module_name + ") failed: " +
-                                            hipGetErrorString(e));
+    const int idx = module_index(*ds, module_name);
+    if (idx >= 0) {
+        // Already loaded: accept only the same image (kernel lookups keep
+        // using the loaded module, so a different image would not take effect).
+        if (ds->module_sizes[idx] == nbytes && ds->module_hashes[idx] == image_hash(image, nbytes)) return C3HIP_OK;
+        return set_error(C3HIP_ERR_INVALID, std::string("code object for module ") + module_name +
+                                                " differs from the image already loaded on device " +
+                                                std::to_string(dev));
     }
-    ds->modules.push_back(m);
-    ds->module_names.push_back(module_name);
-    return C3HIP_OK;
+    return add_module(ds, module_name, image, nbytes, module_name);
 }
 
 int code_object_path(const char* module_name, char* buf, size_t buflen) {

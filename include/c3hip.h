@@ -104,8 +104,10 @@ int c3hip_shutdown(void);
 /*
  * Register a code object image for module `module_name` ("elementwise",
  * "gemm_f32", "gemm_bf16", "reduce" or "loss") on the current device, e.g. one read
- * back from the on-disk JIT cache.  A module already loaded on the device is
- * kept (returns 0); later lookups use whichever image was loaded first.
+ * back from the on-disk JIT cache.  If the module is not loaded yet, the
+ * image is loaded.  If it is, the call returns 0 when `image` is the loaded
+ * image (same bytes) and C3HIP_ERR_INVALID otherwise, since kernel lookups
+ * keep using the loaded module.
  * Replaces the reference's JITCache read path, which reloads cached LLVM
  * bitcode into an ExecutionEngine (src/C3/LinalgElementwiseGen.cpp:403-439).
  */
@@ -230,6 +232,11 @@ int c3hip_linear_fwd_noalloc(int dtype, const void* X, const void* W, const floa
  * C3HIP_ACT_RELU, dY * (Y * (1 - Y)) for C3HIP_ACT_SIGMOID, dY * (1 - Y * Y)
  * for C3HIP_ACT_TANH (the activation's derivative from its output) and
  * dZ = dY for C3HIP_ACT_NONE:
+ * (The inputs hold no pre-activation Z.  For ReLU the mask from Y equals the
+ * reference's Gt(Z, 0) and sigmoid's s from Y equals its recomputation from
+ * Z; the reference's Tanh node instead recomputes t = (e^z - e^-z)/(e^z +
+ * e^-z) from Z, so tanh layers differ from it in the last bits (within 16 ulp
+ * of |dY|) and, for |z| > ~88.7 where its e^z overflows to NaN, give 0.)
  *   dX[M,K] = dZ . W^T,  dW[K,N] = X^T . dZ,  db[N] = sum over rows of dZ.
  * dX, dW and db are each optional (NULL skips it).  dZ is formed inside the
  * GEMM operand loads and never written.  C3HIP_F32: all fp32.  C3HIP_BF16:

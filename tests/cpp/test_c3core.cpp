@@ -5,6 +5,9 @@
 // check the registry, region registry, cost model, JIT cache, hot-path
 // manager, engine watchdog and backward capture behaviour.  Tests named gpu_*
 // run the same flow on HIP device tensors and are invoked by the GPU pytest.
+#include <dirent.h>
+#include <fcntl.h>
+#include <sys/stat.h>
 #include <unistd.h>
 
 #include <algorithm>
@@ -23,6 +26,7 @@
 #include "C3/C3KernelRegistry.h"
 #include "C3/FusionCostModel.h"
 #include "C3/GraphMerger.h"
+#include "C3/HipCompiledKernel.h"
 #include "C3/PGOManager.h"
 #include "C3/JITCache.h"
 #include "C3/RegionFusion.h"
@@ -286,30 +290,141 @@ TEST(jit_cache_layout_and_versioning) {
     CHECK(c.lookup(key).empty());
     CHECK_EQ(c.misses(), m0 + 1);
     std::vector<char> img = {'\x7f', 'E', 'L', 'F', 1, 2, 3};
+    const std::string sha = sha256_hex(img.data(), img.size());
     const std::string path = c.store(key, img, {"module=gemm_f32"});
-    CHECK_EQ(path, dir + "/c3_jit_" + key + ".hsaco");
+    CHECK_EQ(path, dir + "/c3_jit_obj_" + sha + ".hsaco");
     CHECK_EQ(c.stores(), s0 + 1);
     CHECK_EQ(c.lookup(key), path);
-    CHECK_EQ(c.hits(), h0 + 1);
+    CHECK_EQ(c.lookup(key, sha), path);
+    CHECK_EQ(c.hits(), h0 + 2);
     std::vector<char> back;
     CHECK(JITCache::readFile(path, &back) && back == img);
-    std::ifstream meta(dir + "/c3_jit_" + key + ".meta");
-    std::string line;
-    std::getline(meta, line);
-    CHECK_EQ(line, std::string(JITCache::currentJITVersion()));
+    {
+        std::ifstream meta(dir + "/c3_jit_" + key + ".meta");
+        std::string line;
+        std::getline(meta, line);
+        CHECK_EQ(line, std::string(JITCache::currentJITVersion()));
+        std::getline(meta, line);
+        CHECK_EQ(line, "image=" + sha);
+        std::getline(meta, line);
+        CHECK_EQ(line, std::string("module=gemm_f32"));
+    }
     // A stale version evicts the entry.
-    { std::ofstream m(dir + "/c3_jit_" + key + ".meta"); m << "jit_v2\n"; }
+    { std::ofstream m(dir + "/c3_jit_" + key + ".meta"); m << "jit_v2\nimage=" << sha << "\n"; }
     CHECK(c.lookup(key).empty());
-    CHECK(access(path.c_str(), F_OK) != 0);
-    // No temporary files are left behind; evict removes entries.
+    CHECK(access((dir + "/c3_jit_" + key + ".meta").c_str(), F_OK) != 0);
+    // No temporary files are left behind; evict removes entries and objects.
     CHECK(!c.store(key, img).empty());
     c.evict();
     CHECK(c.lookup(key).empty());
+    CHECK(access(path.c_str(), F_OK) != 0);
     setenv("C3_JIT_CACHE_DISABLE", "1", 1);
     CHECK(!JITCache::isEnabled());
     unsetenv("C3_JIT_CACHE_DISABLE");
     CHECK(JITCache::isEnabled());
     unsetenv("C3_AOT_CACHE_DIR");
+}
+
+TEST(jit_cache_one_object_per_image) {
+    // Many spec keys naming the same code object store it once.
+    const std::string dir = tmpdir();
+    setenv("C3_AOT_CACHE_DIR", dir.c_str(), 1);
+    JITCache& c = JITCache::getInstance();
+    std::vector<char> a(100000, 'a'), b(5000, 'b');
+    for (int i = 0; i < 20; ++i) CHECK(!c.store(JITCache::makeKey("spec" + std::to_string(i), 2), i % 2 ? a : b).empty());
+    int objects = 0, metas = 0;
+    DIR* d = opendir(dir.c_str());
+    while (dirent* e = readdir(d)) {
+        const std::string n = e->d_name;
+        if (n.rfind("c3_jit_obj_", 0) == 0) objects++;
+        else if (n.rfind("c3_jit_", 0) == 0 && n.size() > 5 && n.substr(n.size() - 5) == ".meta") metas++;
+        CHECK(n.find(".tmp") == std::string::npos);
+    }
+    closedir(d);
+    CHECK_EQ(objects, 2);
+    CHECK_EQ(metas, 20);
+    for (int i = 0; i < 20; ++i)
+        CHECK_EQ(c.lookup(JITCache::makeKey("spec" + std::to_string(i), 2)),
+                 dir + "/c3_jit_obj_" + sha256_hex(i % 2 ? a.data() : b.data(), i % 2 ? a.size() : b.size()) + ".hsaco");
+    c.evict();
+    unsetenv("C3_AOT_CACHE_DIR");
+}
+
+TEST(jit_cache_rejects_damaged_and_stale_images) {
+    const std::string dir = tmpdir();
+    setenv("C3_AOT_CACHE_DIR", dir.c_str(), 1);
+    JITCache& c = JITCache::getInstance();
+    std::vector<char> img(4096);
+    for (size_t i = 0; i < img.size(); ++i) img[i] = (char)(i * 7);
+    const std::string key = JITCache::makeKey("rh=1|kind=matmul", 2), key2 = JITCache::makeKey("rh=2|kind=matmul", 2);
+    const std::string path = c.store(key, img);
+    CHECK(!c.store(key2, img).empty());
+    const std::string sha = sha256_hex(img.data(), img.size());
+    // An entry recorded for another image (an older build's) is rejected and
+    // evicted; the shared object stays for the other key.
+    const uint64_t r0 = c.rejected();
+    CHECK(c.lookup(key, std::string(64, '0')).empty());
+    CHECK_EQ(c.rejected(), r0 + 1);
+    CHECK(access((dir + "/c3_jit_" + key + ".meta").c_str(), F_OK) != 0);
+    CHECK_EQ(c.lookup(key2, sha), path);
+    // A damaged object (one byte changed, same size) is rejected and removed.
+    {
+        std::fstream f(path, std::ios::in | std::ios::out | std::ios::binary);
+        f.seekp(1000);
+        f.put((char)(img[1000] ^ 0x5a));
+    }
+    struct timespec ts[2] = {{0, UTIME_NOW}, {0, UTIME_NOW}};
+    utimensat(AT_FDCWD, path.c_str(), ts, 0);
+    CHECK(c.lookup(key2, sha).empty());
+    CHECK_EQ(c.rejected(), r0 + 2);
+    CHECK(access(path.c_str(), F_OK) != 0);
+    // Storing again restores a good entry.
+    CHECK_EQ(c.store(key2, img), path);
+    CHECK_EQ(c.lookup(key2, sha), path);
+    c.evict();
+    unsetenv("C3_AOT_CACHE_DIR");
+}
+
+// ------------------------------------------------------ HipCompiledKernel --
+// Borrowed kHIP tensors over host memory (never dereferenced): execute()
+// must refuse operands whose element type differs from the spec's before any
+// HIP call, so a registry hit with mixed operands falls back to eager.
+TEST(hip_kernel_rejects_mixed_dtypes) {
+    std::vector<float> buf(4096);
+    auto hip = [&](std::vector<size_t> shape, DType dt) { return Tensor::fromBlob(buf.data(), std::move(shape), dt, DeviceType::kHIP); };
+    auto throws = [](HipCompiledKernel& k, const std::vector<Tensor>& in, const char* needle) {
+        try {
+            k.execute(in);
+        } catch (const std::runtime_error& e) {
+            return std::string(e.what()).find(needle) != std::string::npos;
+        }
+        return false;
+    };
+    KernelSpec f;
+    f.kind = KernelKind::LinearFwd;
+    f.dtype = DType::kBFloat16;
+    f.act = C3HIP_ACT_RELU;
+    f.input_shapes = {{8, 16}, {16, 8}, {8}};
+    HipCompiledKernel kf(f, 2, "t");
+    CHECK(throws(kf, {hip({8, 16}, DType::kFloat), hip({16, 8}, DType::kBFloat16), hip({8}, DType::kFloat)},
+                 "compiled for bf16"));
+    CHECK(throws(kf, {hip({8, 16}, DType::kBFloat16), hip({16, 8}, DType::kFloat), hip({8}, DType::kFloat)},
+                 "input 1 is fp32"));
+    KernelSpec b;
+    b.kind = KernelKind::LinearBwd;
+    b.dtype = DType::kFloat;
+    b.act = C3HIP_ACT_RELU;
+    b.input_shapes = {{8, 8}, {8, 16}, {16, 8}, {8, 8}};
+    HipCompiledKernel kb(b, 2, "t");
+    CHECK(throws(kb, {hip({8, 8}, DType::kFloat), hip({8, 16}, DType::kFloat), hip({16, 8}, DType::kFloat),
+                      hip({8, 8}, DType::kBFloat16)},
+                 "input 3 is bf16"));
+    KernelSpec m;
+    m.kind = KernelKind::MatMul;
+    m.dtype = DType::kFloat;
+    HipCompiledKernel km(m, 2, "t");
+    CHECK(throws(km, {hip({8, 16}, DType::kFloat), hip({16, 8}, DType::kBFloat16)}, "compiled for fp32"));
+    CHECK(throws(km, {hip({128}, DType::kFloat), hip({16, 8}, DType::kFloat)}, "2-D"));
 }
 
 // ---------------------------------------------------------------- registry --
