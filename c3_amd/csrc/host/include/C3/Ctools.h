@@ -37,8 +37,11 @@ struct ShapeTag {};
 
 // Reference-counted buffer.  kHIP buffers come from a per-process caching
 // pool (hipMalloc on a miss, never returned to the driver until
-// releaseCachedDeviceMemory()); kCPU buffers are plain heap memory.  A
-// borrowed buffer (fromBlob) is never freed.
+// releaseCachedDeviceMemory()) and belong to the stream that was current on
+// the allocating thread: the pool hands a freed block to another stream only
+// after that stream has been made to wait for the block's stream (see
+// Ctools.cpp).  kCPU buffers are plain heap memory.  A borrowed buffer
+// (fromBlob) is never freed.
 class Storage {
 public:
     Storage(size_t nbytes, DeviceType dev);
@@ -56,6 +59,7 @@ private:
     size_t capacity_ = 0;
     DeviceType dev_ = DeviceType::kCPU;
     bool owned_ = true;
+    void* stream_ = nullptr;  // kHIP: stream current at allocation (hipStream_t)
 };
 
 // Free the HIP blocks held by the caching pool (called by shutdownAll).
