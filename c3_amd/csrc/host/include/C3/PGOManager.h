@@ -66,6 +66,13 @@ struct CompilationTask {
 // the current stream and read once they complete (no synchronisation); host
 // kernels are timed by the clock.  No timing while the stream is capturing a
 // graph (the current best candidate runs).
+// Bit reproducibility: while tuning, calls are served by the candidates in
+// turn, and candidates need not add the k range in the same order (a tile
+// forced for tuning never splits an fp32 GEMM over k, while the size
+// heuristic splits small-grid ones; a forced bf16 direct tile splits by its
+// own plan).  So on real-valued data, results may differ in the last bits
+// between calls until the tuner has chosen; from then on one candidate
+// serves every call.  Integer-valued (exactly summed) results never differ.
 class TunedKernel : public CompiledKernel {
 public:
     struct Candidate {

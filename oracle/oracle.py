@@ -220,6 +220,28 @@ def act_grad(y, g, act):
     return out
 
 
+def linear_bwd_from_preact(X, W, Z, dY, act, want=("dX", "dW", "db")):
+    """The reference's per-node backward of a Linear+act layer, from the
+    activation's input Z (the Add output, which the reference's autograd
+    keeps for the activation node): the activation node's rule -- ReLU Gt+Mul
+    (src/C3/C3BackwardCapture.cpp:501-528), Sigmoid and Tanh recomputed from
+    Z through exp (:530-616) -- then MatMul's dX, dW (:681-723) and Add's db
+    (:618-644).  The fused layer backward gets the output Y instead of Z and
+    forms the derivative from Y (act_grad); this composition is what it is
+    compared with."""
+    rule = {0: None, 1: EW_RELU_BWD, 2: EW_SIGMOID_BWD, 3: EW_TANH_BWD}[act]
+    Z, dY = _c(Z), _c(dY)
+    dZ = dY if rule is None else elementwise(rule, Z, dY).reshape(Z.shape)
+    out = [None, None, None]
+    if "dX" in want:
+        out[0] = matmul(dZ, W, transB=True)
+    if "dW" in want:
+        out[1] = matmul(X, dZ, transA=True)
+    if "db" in want:
+        out[2] = sum_reduce(dZ, 0)
+    return tuple(out)
+
+
 def softmax_ce(logits, lbl, want_grad=True, want_rows=False):
     """Mean CE loss and dlogits (None unless want_grad); with want_rows the
     per-row losses are returned as a third value."""

@@ -173,3 +173,38 @@ def test_linear_sigmoid_tanh_bf16(gpu, stream, act):
     assert_close_gemm(host(dX), rX, gemm_bound(dZ, W.T, Nn), 1e-2, out_round=2.0 ** -8, what="dX bf16")
     assert_close_gemm(host(dW), rW, gemm_bound(X.T, dZ, M), 1e-2, what="dW bf16")
     assert_close_gemm(host(db), rb, 2.02 * M * U * np.abs(dZ.astype(np.float64)).sum(0), 1e-2, what="db bf16")
+
+
+@pytest.mark.parametrize("act", [N.ACT_SIGMOID, N.ACT_TANH])
+def test_linear_act_backward_against_reference_composition(gpu, stream, act):
+    """The fused backward (derivative from the saved output Y) against the
+    reference's per-node composition from the pre-activation Z
+    (oracle.linear_bwd_from_preact: the activation node's rule recomputed
+    from Z through exp, then MatMul and Add backward).  Sigmoid: the same dZ
+    bits, so only the GEMM orders differ.  Tanh: dZ differs by at most 16 ulp
+    of |dY| (+ 4 ulp) while |z| <= 88, which adds |dZ err| . |W| to the bound."""
+    M, K, Nn = 256, 192, 320
+    X = O.normal(640, (M, K))
+    W = O.normal(641, (K, Nn), 0.0, 2.0 / np.sqrt(K))
+    b = O.normal(642, Nn, 0.0, 0.5)
+    dY = O.normal(643, (M, Nn))
+    Y = empty((M, Nn))
+    N.linear_fwd(N.F32, ptr(dev(X)), ptr(dev(W)), ptr(dev(b)), ptr(Y), M, K, Nn, act, stream)
+    gY = host(Y)
+    dX, dW, db = empty((M, K)), empty((K, Nn)), empty(Nn)
+    N.linear_bwd(N.F32, ptr(dev(X)), ptr(dev(W)), ptr(Y), ptr(dev(dY)), ptr(dX), ptr(dW), ptr(db), M, K, Nn, act,
+                 stream)
+    Z = O.bias_act(O.matmul(X, W), b, act=0)
+    assert np.max(np.abs(Z)) <= 88.0
+    rX, rW, rb = O.linear_bwd_from_preact(X, W, Z, dY, act)
+    dZ = O.act_grad(gY, dY, act)
+    dz_err = np.abs(dY).astype(np.float64) * 16 * 2.0 ** -23 + 4 * ulp(dZ) if act == N.ACT_TANH else 0.0 * dZ
+    # The GPU's Y differs from tanhf/sigmoid of the oracle's Z by the GEMM bound x slope + a few ulp.
+    y_err = ACT_SLOPE[act] * gemm_bound(X, W, K) + ACT_FWD_ULP[act] * ulp(gY)
+    dz_err = dz_err + 2.0 * np.abs(dY).astype(np.float64) * y_err
+    assert_close_gemm(host(dX), rX, gemm_bound(dZ, W.T, Nn) + dz_err @ np.abs(W.T.astype(np.float64)), FP32_TOL,
+                      what="dX")
+    assert_close_gemm(host(dW), rW, gemm_bound(X.T, dZ, M) + np.abs(X.T.astype(np.float64)) @ dz_err, FP32_TOL,
+                      what="dW")
+    assert_close_gemm(host(db), rb, 2.02 * M * U * np.abs(dZ.astype(np.float64)).sum(0) + dz_err.sum(0), FP32_TOL,
+                      what="db")

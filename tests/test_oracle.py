@@ -445,3 +445,37 @@ def test_act_grad_and_epilogue_activations():
     gz = O.normal(96, z.shape)
     y2 = O.bias_act(t, b, act=2)
     assert np.array_equal(O.act_grad(y2, gz, 2), O.elementwise(O.EW_SIGMOID_BWD, z, gz).reshape(z.shape))
+
+
+def test_fused_tanh_backward_against_the_reference_composition():
+    """The fused Linear+Tanh backward forms tanh' from the saved output Y as
+    1 - Y*Y; the reference's Tanh node recomputes t from the pre-activation z
+    through exp.  For |z| <= 88 they agree within 16 ulp of |g| (plus 4 ulp of
+    the result); beyond that the reference's e^z overflows, t = inf/inf = NaN,
+    while 1 - Y*Y = 0 (the derivative underflows there).  Both facts are pinned."""
+    f = np.float32
+    z = np.concatenate([O.normal(97, 20000, 0.0, 3.0), np.array([88.0, -88.0, 89.0, -89.0, 100.0, -1e4], f)])
+    g = O.normal(98, z.size, 0.0, 2.0)
+    y = O.elementwise(O.EW_TANH, z)
+    fused = O.act_grad(y, g, 3)
+    with np.errstate(all="ignore"):
+        ref = O.elementwise(O.EW_TANH_BWD, z, g)
+    small = np.abs(z) <= 88.0
+    bound = np.abs(g[small]).astype(np.float64) * 16 * 2.0 ** -23 + 4 * _ulp(ref[small])
+    assert np.all(np.abs(fused[small].astype(np.float64) - ref[small]) <= bound)
+    big = np.abs(z) >= 89.0
+    assert np.all(np.isnan(ref[big])) and np.all(fused[big] == 0.0)
+    # The composition routine applies the same rule before its GEMMs.
+    X = O.normal(99, (6, 5))
+    W = O.normal(100, (5, 4))
+    Z = O.normal(101, (6, 4), 0.0, 2.0)
+    dY = O.normal(102, (6, 4))
+    dX, dW, db = O.linear_bwd_from_preact(X, W, Z, dY, 3)
+    dZ = O.elementwise(O.EW_TANH_BWD, Z, dY).reshape(Z.shape)
+    assert np.array_equal(dX, O.matmul(dZ, W, transB=True))
+    assert np.array_equal(dW, O.matmul(X, dZ, transA=True))
+    assert np.array_equal(db, O.sum_reduce(dZ, 0))
+    # ReLU: the mask from Z equals the mask from Y = maxnum(Z, 0), so both routes agree bit for bit.
+    Y = O.bias_act(Z, np.zeros(4, f), act=1)
+    for a, b in zip(O.linear_bwd_from_preact(X, W, Z, dY, 1), O.linear_bwd(X, W, Y, dY, 1)):
+        assert np.array_equal(a, b)
