@@ -33,6 +33,7 @@ struct GemmArgs {
     int _pad;
     int64_t split_k;    // split-K: k extent of one split (blockIdx.y = split), 0 = none
     int64_t c_split;    // split-K: elements between the fp32 outputs of consecutive splits
+    void* dz;           // dx_mask_dz kinds: the masked A operand (dZ) is also written here (A's layout), or null
 };
 
 // Blocks are handed to the 8 XCDs round-robin (block i runs on XCD i % 8).

@@ -59,10 +59,12 @@ struct TileLoader {
 
     f32x4 r[NV];
     uint32_t off0;   // element offset of vector 0 at k-tile 0
+    uint32_t ld_;    // leading dimension (elements)
     int row0;        // tile-relative row of vector 0 (KC) / row of the vector (!KC)
     int kk0;         // tile-relative k of vector 0
 
     __device__ __forceinline__ void init(int tid, int64_t ld, int64_t grow0) {
+        ld_ = (uint32_t)ld;
         if (KC) {
             row0 = tid >> 2;
             kk0 = 4 * (tid & 3);
@@ -110,6 +112,28 @@ struct TileLoader {
         }
     }
 
+    // Write the staged (masked) values to global memory at the operand's own
+    // offsets in D (advanced to the same k-tile as the load), in-range
+    // elements only: the dx_mask_dz kinds write dZ this way.
+    __device__ __forceinline__ void store_global(float* __restrict__ D, int64_t rows_left, int64_t k_left) const {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int rr = KC ? row0 + i * RSTEP : row0;
+            const int kk = KC ? kk0 : kk0 + i * KSTEP;
+            const uint32_t off = off0 + (KC ? (uint32_t)(i * RSTEP) * ld_ : (uint32_t)(i * KSTEP) * ld_);
+            if (VEC) {
+                if (rr < rows_left && kk < k_left) *(f32x4*)(D + off) = r[i];
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int er = KC ? rr : rr + e;
+                    const int ek = KC ? kk + e : kk;
+                    if (er < rows_left && ek < k_left) D[off + (uint32_t)e] = r[i][e];
+                }
+            }
+        }
+    }
+
     __device__ __forceinline__ void store(float* __restrict__ S) const {
         constexpr int STRIDE = Lds<ROWS, KC>::STRIDE;
 #pragma unroll
@@ -139,8 +163,12 @@ __device__ __forceinline__ void read_frag(const float* __restrict__ S, int r0, i
 }
 
 // bid: this block's index among the GEMM's blocks (see tile_coords).
+// DZ: also write the masked A operand to p.dz.  Block (tm, tn) writes the
+// k-tiles kt with kt % (column tiles) == tn of its rows, so every k-tile of
+// every row tile is written once and the writes are spread evenly over the
+// blocks; each is written from the registers that stage it into LDS.
 template <int BM, int BN, int WAVES_M, int WAVES_N, bool AK, bool BKC, bool AMASK, bool BMASK,
-          bool DB, bool VEC>
+          bool DB, bool VEC, bool DZ = false>
 __device__ __forceinline__ void gemm_f32_body(const GemmArgs& p, int bid) {
     constexpr int NT = 64 * WAVES_M * WAVES_N;
     constexpr int TM = BM / WAVES_M, TN = BN / WAVES_N;
@@ -189,8 +217,11 @@ __device__ __forceinline__ void gemm_f32_body(const GemmArgs& p, int bid) {
     float dbacc = 0.0f;
 
     const int nk = (int)((p.K + kBK - 1) / kBK);
+    float* __restrict__ Dz = (float*)p.dz;
+    const int nbn = (int)((p.N + BN - 1) / BN);
     la.load(A, Am, lda, a_rows, p.K);
     lb.load(B, Bm, ldb, b_rows, p.K);
+    if (DZ && tn == 0) la.store_global(Dz, a_rows, p.K);
     la.store(smem);
     lb.store(smem + A_SIZE);
     __syncthreads();
@@ -236,6 +267,8 @@ __device__ __forceinline__ void gemm_f32_body(const GemmArgs& p, int bid) {
 
         if (more) {
             float* Ns = smem + (cur ^ 1) * STAGE;
+            if (DZ && (kt + 1) % nbn == tn)
+                la.store_global(Dz + (int64_t)(kt + 1) * a_kstep, a_rows, p.K - (int64_t)(kt + 1) * kBK);
             la.store(Ns);
             lb.store(Ns + A_SIZE);
         }
@@ -320,20 +353,24 @@ __device__ __forceinline__ GemmArgs split_args_f32(const GemmArgs& p) {
 // One extern "C" symbol per (layout, fusion, tile, vector) case.
 // Tile suffix _tBMxBN_wWMxWN; _v: vectorised operand loads (contiguous extent
 // % 4 == 0 and 16-byte aligned bases), _s: scalar loads.
-#define C3_GEMM_F32_ONE(NAME, BM, BN, WM, WN, OCC, AK, BKC, AMASK, BMASK, DB)                         \
-    extern "C" __global__ __launch_bounds__(64 * WM * WN, OCC) void NAME##_v(GemmArgs p) {                     \
-        gemm_f32_body<BM, BN, WM, WN, AK, BKC, AMASK, BMASK, DB, true>(split_args_f32<AK, BKC>(p), blockIdx.x);  \
-    }                                                                                                         \
-    extern "C" __global__ __launch_bounds__(64 * WM * WN, OCC) void NAME##_s(GemmArgs p) {                     \
-        gemm_f32_body<BM, BN, WM, WN, AK, BKC, AMASK, BMASK, DB, false>(split_args_f32<AK, BKC>(p), blockIdx.x); \
+#define C3_GEMM_F32_ONE_DZ(NAME, BM, BN, WM, WN, OCC, AK, BKC, AMASK, BMASK, DB, DZ)                              \
+    extern "C" __global__ __launch_bounds__(64 * WM * WN, OCC) void NAME##_v(GemmArgs p) {                         \
+        gemm_f32_body<BM, BN, WM, WN, AK, BKC, AMASK, BMASK, DB, true, DZ>(split_args_f32<AK, BKC>(p), blockIdx.x);  \
+    }                                                                                                             \
+    extern "C" __global__ __launch_bounds__(64 * WM * WN, OCC) void NAME##_s(GemmArgs p) {                         \
+        gemm_f32_body<BM, BN, WM, WN, AK, BKC, AMASK, BMASK, DB, false, DZ>(split_args_f32<AK, BKC>(p), blockIdx.x); \
     }
+#define C3_GEMM_F32_ONE(NAME, BM, BN, WM, WN, OCC, AK, BKC, AMASK, BMASK, DB) \
+    C3_GEMM_F32_ONE_DZ(NAME, BM, BN, WM, WN, OCC, AK, BKC, AMASK, BMASK, DB, false)
 
 // Kinds: fwd (A=X k-contig, B=W [K,N]); dx/dx_mask (A=dY[, masked by Y], B=W as [N][K]);
-// dw/dw_mask (A=X^T, B=dY[, masked]; db side output); tt (A^T . B^T).
+// dx_mask_dz (dx_mask that also writes dZ = the masked dY); dw/dw_mask (A=X^T,
+// B=dY[, masked]; db side output); tt (A^T . B^T).
 #define C3_GEMM_F32_KINDS(T, BM, BN, WM, WN, OCC)                                                    \
     C3_GEMM_F32_ONE(c3_gemm_f32_fwd_##T, BM, BN, WM, WN, OCC, true, false, false, false, false)      \
     C3_GEMM_F32_ONE(c3_gemm_f32_dx_##T, BM, BN, WM, WN, OCC, true, true, false, false, false)        \
     C3_GEMM_F32_ONE(c3_gemm_f32_dx_mask_##T, BM, BN, WM, WN, OCC, true, true, true, false, false)    \
+    C3_GEMM_F32_ONE_DZ(c3_gemm_f32_dx_mask_dz_##T, BM, BN, WM, WN, OCC, true, true, true, false, false, true) \
     C3_GEMM_F32_ONE(c3_gemm_f32_dw_##T, BM, BN, WM, WN, OCC, false, false, false, false, true)       \
     C3_GEMM_F32_ONE(c3_gemm_f32_dw_mask_##T, BM, BN, WM, WN, OCC, false, false, false, true, true)   \
     C3_GEMM_F32_ONE(c3_gemm_f32_tt_##T, BM, BN, WM, WN, OCC, false, true, false, false, false)

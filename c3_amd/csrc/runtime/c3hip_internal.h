@@ -42,6 +42,7 @@ struct GemmArgs {
     int _pad;
     int64_t split_k;
     int64_t c_split;
+    void* dz;
 };
 
 // Argument block of c3_gemm_f32_bwd[_mask]_t64x64_* (mirrors BwdPairArgs in

@@ -44,7 +44,7 @@ bool ew_is_binary(int op) {
 
 // ---- GEMM planning -------------------------------------------------------
 
-enum class Kind { Fwd, FwdT, Dx, DxMask, Dw, DwMask, DwB, TT };
+enum class Kind { Fwd, FwdT, Dx, DxMask, DxMaskDz, Dw, DwMask, DwB, TT };
 
 const char* kind_name(Kind k) {
     switch (k) {
@@ -52,6 +52,7 @@ const char* kind_name(Kind k) {
         case Kind::FwdT: return "fwdt";
         case Kind::Dx: return "dx";
         case Kind::DxMask: return "dx_mask";
+        case Kind::DxMaskDz: return "dx_mask_dz";
         case Kind::Dw: return "dw";
         case Kind::DwMask: return "dw_mask";
         case Kind::DwB: return "dwb";
@@ -102,7 +103,7 @@ const Tile* choose_f32_tile(Kind kind, int64_t M, int64_t N) {
         if (const Tile* t = find_tile(kF32Tiles, nt, forced)) return t;
     }
     const bool dw = kind == Kind::Dw || kind == Kind::DwMask;
-    const bool dx = kind == Kind::Dx || kind == Kind::DxMask;
+    const bool dx = kind == Kind::Dx || kind == Kind::DxMask || kind == Kind::DxMaskDz;
     const int64_t blocks256 = ((M + 255) / 256) * ((N + 127) / 128);
     const int64_t blocks_wide = ((M + 127) / 128) * ((N + 255) / 256);
     if (dx && blocks_wide >= 256) return &kF32Tiles[3];
@@ -300,7 +301,7 @@ bool vec_ok(bool kc, int64_t rows, int64_t k, int64_t ld, const void* p, const v
 // forced tile never splits.
 int plan_split_f32(const GemmArgs& a, const Tile* t) {
     if (!t_tile_f32.empty() || std::getenv("C3_HIP_GEMM_TILE")) return 0;
-    if (t->bm != 64 || a.db != nullptr || a.K < 512) return 0;
+    if (t->bm != 64 || a.db != nullptr || a.dz != nullptr || a.K < 512) return 0;
     const int64_t tiles = tile_count(a, t);
     if (tiles >= 32) return 0;
     int64_t S = std::min<int64_t>(256 / tiles, a.K / 128);
@@ -787,6 +788,29 @@ int c3hip_linear_bwd(int dtype, const void* X, const void* W, const void* Y, con
     if (dX && dW && M > 0 && N > 0 && K > 0) {
         rc = linear_bwd_pair(ax, aw, relu, stream);
         if (rc != C3HIP_ERR_UNSUPPORTED) return rc;  // launched (or failed); unsupported: separate launches
+        clear_error();
+    }
+    if (relu && dX && dW && M > 0 && N > 0 && K > 0) {
+        // Both GEMMs: dX forms dZ = mask(Y) * dY in its operand loads anyway,
+        // so it also writes dZ (each k-tile once, from the staging registers)
+        // and dW + db run on dZ as a plain GEMM, which reads 4 bytes per
+        // element of the k = M operand instead of 8 (dY and Y).  The products
+        // are the same IEEE operations, so every output has the bits of the
+        // masked launches.  Without memory for dZ, the masked launches run.
+        void* dz = nullptr;
+        bool owned = false;
+        if (take_workspace(nullptr, (size_t)(M * N) * sizeof(float), stream, &dz, &owned, "dZ") == C3HIP_OK) {
+            GemmArgs a1 = ax;
+            a1.dz = dz;
+            rc = run_gemm(dtype, Kind::DxMaskDz, a1, true, true, stream);
+            if (rc == C3HIP_OK) {
+                GemmArgs a2 = aw;
+                a2.B = dz;
+                a2.Bmask = nullptr;
+                rc = run_gemm(dtype, Kind::Dw, a2, false, false, stream);
+            }
+            return release_workspace(dz, owned, rc, stream, "dZ");
+        }
         clear_error();
     }
     if (dX) {

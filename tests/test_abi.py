@@ -48,7 +48,7 @@ def _kernel_symbols(hsaco: Path):
 
 def test_code_objects_hold_every_dispatched_kernel():
     gemm = _kernel_symbols(LIB / "gemm_f32.hsaco")
-    for kind in ["fwd", "dx", "dx_mask", "dw", "dw_mask", "tt"]:
+    for kind in ["fwd", "dx", "dx_mask", "dx_mask_dz", "dw", "dw_mask", "tt"]:
         for tile in ["t64x64", "t128x128", "t256x128", "t128x256"]:
             for v in "vs":
                 assert f"c3_gemm_f32_{kind}_{tile}_{v}" in gemm

@@ -188,6 +188,28 @@ def test_every_fp32_tile_bit_exact(gpu, stream, monkeypatch, tile, M, K, Nn):
     same_bits(gb, rb)
 
 
+@pytest.mark.parametrize("tile", [None, "t64x64", "t128x128", "t256x128", "t128x256"])
+@pytest.mark.parametrize("M,K,Nn", [(1024, 768, 1536), (300, 260, 200), (2048, 1024, 4096)])
+def test_bwd_dz_side_output_matches_masked_launches(gpu, stream, monkeypatch, tile, M, K, Nn):
+    # With dX and dW both asked for, the dX kernel also writes dZ = mask(Y) dY
+    # and dW + db run on it unmasked; alone, each runs with the mask in its
+    # operand loads.  Real-valued inputs: both routes must agree bit for bit.
+    if tile:
+        monkeypatch.setenv("C3_HIP_GEMM_TILE", tile)
+    X = O.normal(81, (M, K))
+    W = O.normal(82, (K, Nn), 0.0, 1.0 / np.sqrt(K))
+    Y = O.normal(83, (M, Nn))          # the saved output: mixed signs, exact zeros of both signs
+    Y[::7, ::5] = 0.0
+    Y[3::11, 1::9] = -0.0
+    dY = O.normal(84, (M, Nn))
+    both = _run_bwd(stream, X, W, Y, dY, 1)
+    gx = _run_bwd(stream, X, W, Y, dY, 1, ("dX",))[0]
+    _, gw, gb = _run_bwd(stream, X, W, Y, dY, 1, ("dW", "db"))
+    same_bits(both[0], gx)
+    same_bits(both[1], gw)
+    same_bits(both[2], gb)
+
+
 @pytest.mark.parametrize("M,K,Nn", BWD_SHAPES)
 @pytest.mark.parametrize("act", [1, 0])
 def test_linear_bwd_integer_bit_exact(gpu, stream, M, K, Nn, act):
