@@ -186,40 +186,26 @@ def main():
     def fwd():
         C.linear_fwd(C.F32, X.data_ptr(), W.data_ptr(), b.data_ptr(), Y.data_ptr(), M, K, N, C.ACT_RELU, s)
 
-    def bwd_dx():
-        C.linear_bwd(C.F32, X.data_ptr(), W.data_ptr(), Y.data_ptr(), dY.data_ptr(), dX.data_ptr(), None, None,
-                     M, K, N, C.ACT_RELU, s)
-
-    def bwd_dw():
-        C.linear_bwd(C.F32, X.data_ptr(), W.data_ptr(), Y.data_ptr(), dY.data_ptr(), None, dW.data_ptr(),
+    def bwd():
+        C.linear_bwd(C.F32, X.data_ptr(), W.data_ptr(), Y.data_ptr(), dY.data_ptr(), dX.data_ptr(), dW.data_ptr(),
                      db.data_ptr(), M, K, N, C.ACT_RELU, s)
 
-    # A step is the forward and the full backward; the backward is issued as
-    # its two kernels so events can bracket each (same launches as one
-    # c3hip_linear_bwd call with dX, dW and db).
-    kernels = [("gemm_fwd_bias_relu", fwd), ("gemm_dx_mask", bwd_dx), ("gemm_dw_mask_db", bwd_dw)]
-    for _ in range(args.warmup):
-        for _, fn in kernels:
-            fn()
-    torch.cuda.synchronize()
+    # A step is c3hip_linear_fwd + c3hip_linear_bwd (dX, dW, db): the forward
+    # GEMM, then the dX GEMM (which also writes dZ) and the dW + db GEMM on dZ.
+    # Each launch is timed on its stream by the library's launch timing.
+    def step():
+        fwd()
+        bwd()
 
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(kernels) + 1)] for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        ev[i][0].record(stream)
-        for j, (_, fn) in enumerate(kernels):
-            fn()
-            ev[i][j + 1].record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    per_kernel_ms = {name: sum(ev[i][j].elapsed_time(ev[i][j + 1]) for i in range(args.steps)) / args.steps
-                     for j, (name, _) in enumerate(kernels)}
-    step_ms = sum(ev[i][0].elapsed_time(ev[i][-1]) for i in range(args.steps)) / args.steps
+    for _ in range(args.warmup):
+        step()
+    step_ms, wall, kt = _timed_steps(torch, C, stream, step, args.steps)
     flop_step = 6.0 * M * N * K
     value = flop_step / (step_ms * 1e-3) / 1e12
     wall_tflops = flop_step * args.steps / wall / 1e12
+    per_kernel_ms = {k: v["avg_ms"] for k, v in kt.items()}
 
+    # Each of the three GEMMs does 2 M N K flop per launch.
     dom = max(per_kernel_ms, key=per_kernel_ms.get)
     dom_ms = per_kernel_ms[dom]
     dom_achieved = 2.0 * M * N * K / (dom_ms * 1e-3) / 1e12
@@ -256,10 +242,47 @@ def main():
         out["mlp_784_256_128_10_fp32"] = bench_mlp(torch, C, dev, s, [784, 256, 128, 10], 128, C.F32,
                                                    steps=200, uniform_x=True, graph=True)
         out["mlp_deep_bf16"] = bench_mlp(torch, C, dev, s, [4096, 8192, 8192, 8192, 4096, 1000], 16384, C.BF16,
-                                         steps=10, uniform_x=False)
+                                         steps=10, uniform_x=False, timed_kernels=True)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out), flush=True)
+
+
+def _timed_steps(torch, C, stream, step, steps):
+    """Time `steps` back-to-back steps with HIP events on `stream` (the step
+    time, and the host wall time), then the same number again with the
+    library's launch timing on, for each kernel's duration (events around
+    every launch add a little time between kernels, so that second loop does
+    not give the step time).  Returns (ms per step, wall s, kernel table)."""
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    step_ms = e0.elapsed_time(e1) / steps
+    C.set_launch_timing(True)
+    try:
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+        kt = _kernel_table(C.launch_timings(), steps)
+    finally:
+        C.set_launch_timing(False)
+    return step_ms, wall, kt
+
+
+def _kernel_table(records, steps):
+    """Per kernel name: launches per step, mean and total duration per step (ms),
+    from the library's launch timing records [(name, ms), ...] of `steps` steps."""
+    agg = {}
+    for name, ms in records:
+        agg.setdefault(name, []).append(ms)
+    return {n: {"launches_per_step": round(len(v) / steps, 3), "avg_ms": round(sum(v) / len(v), 4),
+                "ms_per_step": round(sum(v) / steps, 4)} for n, v in agg.items()}
 
 
 def _traffic(kernel: str):
@@ -269,7 +292,9 @@ def _traffic(kernel: str):
     try:
         for line in p.read_text().splitlines():
             if line.startswith("traffic-json:"):
-                return json.loads(line.split(":", 1)[1]).get(kernel, {}).get("bytes_per_launch")
+                for entry in json.loads(line.split(":", 1)[1]).values():
+                    if entry.get("kernel") == kernel:
+                        return entry.get("bytes_per_launch")
     except (ValueError, OSError):
         pass
     return None
@@ -295,17 +320,18 @@ def bench_bf16(torch, C, dev, s, args):
 
     for _ in range(args.warmup):
         step()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    e0.record()
-    for _ in range(args.steps):
-        step()
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / args.steps
+    ms, _, kt = _timed_steps(torch, C, torch.cuda.current_stream(), step, args.steps)
     tf = 6.0 * M * N * K / (ms * 1e-3) / 1e12
+    # The three GEMMs (forward, dX, dW) each do 2 M N K flop per launch; the
+    # backward pre-pass (dZ and the db partials) and the db reduction are HBM streams.
+    gemms = {k: v for k, v in kt.items() if k.startswith("c3_gemm_")}
+    dom = max(gemms, key=lambda k: gemms[k]["avg_ms"])
+    ach = 2.0 * M * N * K / (gemms[dom]["avg_ms"] * 1e-3) / 1e12
     return {"workload": "same layer, bf16 storage, fp32 accumulate", "ms_per_step": round(ms, 4),
-            "tflops": round(tf, 2), "frac_of_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4)}
+            "tflops": round(tf, 2), "frac_of_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4), "kernels": kt,
+            "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(ach, 2), "peak": PEAK_BF16_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(ach / PEAK_BF16_TFLOPS, 4),
+                         "avg_launch_ms": gemms[dom]["avg_ms"], "traffic": None}}
 
 
 def bench_elementwise(torch, C, dev, s, n, sets, iters=10):
@@ -447,7 +473,7 @@ def bench_bf16_sweep(torch, C, dev, s, reps=5, groups=3, warmup=3):
             "median_tflops": vals[len(vals) // 2], "min_tflops": vals[0], "max_tflops": vals[-1]}
 
 
-def bench_mlp(torch, C, dev, s, dims, batch, dtype, steps, uniform_x, graph=False):
+def bench_mlp(torch, C, dev, s, dims, batch, dtype, steps, uniform_x, graph=False, timed_kernels=False):
     """Train step of an MLP (ReLU between layers, softmax-CE, SGD) through the
     dispatch flow (c3_amd/trainer.py: region kernels from RegionFusionRegistry,
     fused backwards from C3BackwardCapture, JIT cache warm), after warm-up
@@ -484,6 +510,17 @@ def bench_mlp(torch, C, dev, s, dims, batch, dtype, steps, uniform_x, graph=Fals
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms = e0.elapsed_time(e1) / steps
+    kt = None
+    if timed_kernels:
+        # The same steps again with every launch timed (kernel durations only).
+        C.set_launch_timing(True)
+        try:
+            for _ in range(steps):
+                tr.step(xd.data_ptr(), lbl.data_ptr(), lr, False, s)
+            torch.cuda.synchronize()
+            kt = _kernel_table(C.launch_timings(), steps)
+        finally:
+            C.set_launch_timing(False)
     loss1 = tr.step(xd.data_ptr(), lbl.data_ptr(), lr, True, s)
     st1 = tr.stats()
     graph_ms = None
@@ -512,7 +549,17 @@ def bench_mlp(torch, C, dev, s, dims, batch, dtype, steps, uniform_x, graph=Fals
     flop = 6.0 * sum(macs) - 2.0 * macs[0]
     tf = flop / (ms * 1e-3) / 1e12
     peak = PEAK_FP32_TFLOPS if dtype == C.F32 else PEAK_BF16_TFLOPS
-    return {"dims": dims, "batch": batch, "dtype": "fp32" if dtype == C.F32 else "bf16",
+    extra = {}
+    if kt is not None:
+        # The step's GEMM flop (every layer's forward and dW, every layer's dX
+        # but the first) over the summed durations of its GEMM launches.
+        gemm_ms = sum(v["ms_per_step"] for k, v in kt.items() if k.startswith("c3_gemm_"))
+        ach = flop / (gemm_ms * 1e-3) / 1e12
+        extra = {"kernels": kt, "roofline": {
+            "bound": "mfma", "kernel": "all GEMM launches of the step", "achieved": round(ach, 2), "peak": peak,
+            "unit": "TFLOP/s", "frac": round(ach / peak, 4), "gemm_ms_per_step": round(gemm_ms, 4),
+            "traffic": None}}
+    return {**extra, "dims": dims, "batch": batch, "dtype": "fp32" if dtype == C.F32 else "bf16",
             "ms_per_step": round(ms, 4), "us_per_step_wall": round(wall / steps * 1e6, 1),
             "tflops": round(tf, 3), "frac_of_peak": round(tf / peak, 4), "flop_per_step": flop,
             "input_grad": "not computed for the first layer (its input is the data batch)",
@@ -527,43 +574,109 @@ def bench_mlp(torch, C, dev, s, dims, batch, dtype, steps, uniform_x, graph=Fals
 
 def cpu_baseline():
     """The oracle (C restatement of the reference's JIT'd loops: 64x64 i/j
-    tiles, sequential k, no FMA) on one host core, over a slice of the same
-    layer: 32 rows of Y (forward), 32 rows of dX and 32 rows of dW (about
-    15 s on one core).  Each output row of a GEMM costs the same, so the
-    slice rate is the full layer's rate: TFLOP/s = slice flop / slice seconds."""
+    tiles, sequential k, no FMA), run on the host, for every workload in
+    the bench: the headline layer and both sweeps on row slices (each output
+    row of a GEMM costs the same, so a slice's rate is the whole layer's;
+    the extrapolated full-step time is stated), the small MLP's full train
+    step, and the eight elementwise ops.  One core, as the reference runs
+    its GEMM kernels (serially, src/C3/C3Engine.cpp:168); relu-bwd, a
+    two-node graph the reference runs on up to 8 threads for n >= 262144
+    (src/C3/C3Engine.cpp:165-206), also on min(cores, 8) threads."""
     import numpy as np
 
     from oracle import oracle as O
 
-    rows = 32
-    X = O.normal(1, (rows, K))
-    W = O.normal(2, (K, N), 0.0, 1.0 / 64.0)
-    b = O.normal(3, N, 0.0, 0.1)
-    dY = O.normal(4, (rows, N))
-    Xm = O.normal(5, (M, rows))      # X[:, k-slice] for the dW rows
-    dZm = O.normal(6, (M, N))        # dZ for the dW slice
+    t_all = time.perf_counter()
+    head = _cpu_layer_slices(O, np, M, K, N, rows=16)
+    out = {"value": round(head["tflops"], 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
+           "sample": f"oracle on {head['rows']} rows of Y, of dX and of dW of the {M}x{K}x{N} fp32 layer, one "
+                     f"core ({head['sample_s']:.1f} s); the full fwd+bwd step extrapolates to "
+                     f"{head['full_step_s'] / 3600:.2f} h",
+           "host_cpu": _cpu_model(),
+           "mlp_784_256_128_10_fp32": _cpu_mlp(O, np),
+           "elementwise": _cpu_elementwise(O, np),
+           "bf16_sweep": _cpu_sweep(O, np),
+           "mlp_deep_bf16": _cpu_deep_mlp(O, np)}
+    out["total_cpu_s"] = round(time.perf_counter() - t_all, 1)
+    return out
+
+
+def _fill(np, shape, seed, scale=1.0):
+    """Normal-looking values for timing runs (no denormals): a seeded block
+    tiled over the shape (generating every element would dominate the run)."""
+    blk = np.random.default_rng(seed).standard_normal(1 << 16).astype(np.float32) * scale
+    return np.resize(blk, shape).astype(np.float32)
+
+
+def _cpu_layer_slices(O, np, m, k, n, rows):
+    """Oracle time of `rows` rows of Y (forward with bias and ReLU), `rows`
+    rows of dX (dZ . W^T) and `rows` rows of dW (X^T . dZ, a full sequential
+    k = m sum each) of an m x k x n layer, with the full layer's leading
+    dimensions; the full step is m / rows forward and dX slices and k / rows
+    dW slices."""
+    X = _fill(np, (rows, k), 1)
+    W = _fill(np, (k, n), 2, 1.0 / 64.0)
+    b = _fill(np, n, 3, 0.1)
+    dZ = _fill(np, (rows, n), 4)
+    Xk = _fill(np, (m, rows), 5)       # X[:, k-slice] for the dW rows
+    dZm = _fill(np, (m, n), 6)
     t0 = time.perf_counter()
-    Y = O.linear_fwd(X, W, b, 1)
+    O.linear_fwd(X, W, b, 1)
     t1 = time.perf_counter()
-    dZ = O.relu_mask_mul(Y, dY)
     O.matmul(dZ, W, transB=True)
     t2 = time.perf_counter()
-    O.matmul(Xm, dZm, transA=True)
+    O.matmul(Xk, dZm, transA=True)
     t3 = time.perf_counter()
-    flop = 2.0 * rows * N * K * 2 + 2.0 * rows * M * N
-    secs = t3 - t0
-    return {"value": round(flop / secs / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
-            "sample": f"oracle on {rows} rows of Y ({t1 - t0:.1f}s), {rows} rows of dX ({t2 - t1:.1f}s) and "
-                      f"{rows} rows of dW ({t3 - t2:.1f}s) of the {M}x{K}x{N} layer, one core; "
-                      f"full fwd+bwd step extrapolates to {6.0 * M * N * K / (flop / secs) / 3600:.1f} h",
-            "host_cpu": _cpu_model(),
-            "mlp_784_256_128_10_fp32": _cpu_mlp(O, np),
-            "elementwise_2^24": _cpu_elementwise(O, np)}
+    full = (t1 - t0) * m / rows + (t2 - t1) * m / rows + (t3 - t2) * k / rows
+    return {"rows": rows, "sample_s": t3 - t0, "full_step_s": full, "tflops": 6.0 * m * n * k / full / 1e12}
 
 
-def _cpu_mlp(O, np, reps=5):
+def _cpu_sweep(O, np):
+    """The bf16 sweep on the oracle (bf16 values widened to fp32 run the same
+    loops): 1024x1024x1024 as a full fwd + bwd step (dZ from the ReLU mask),
+    the other 26 shapes by one-row slices as in _cpu_layer_slices."""
+    m = k = n = 1024
+    X, W = O.round_bf16(_fill(np, (m, k), 11)), O.round_bf16(_fill(np, (k, n), 12, 1.0 / 32.0))
+    b, dY = _fill(np, n, 13, 0.1), O.round_bf16(_fill(np, (m, n), 14))
+    t0 = time.perf_counter()
+    Y = O.linear_fwd(X, W, b, 1)
+    O.linear_bwd(X, W, Y, dY, 1)
+    full = time.perf_counter() - t0
+    res = {"1024x1024x1024": {"full_step_s": round(full, 3), "tflops": round(6.0 * m * n * k / full / 1e12, 6),
+                              "sample": "full step"}}
+    for (mm, kk, nn) in SWEEP:
+        if (mm, kk, nn) == (1024, 1024, 1024):
+            continue
+        r = _cpu_layer_slices(O, np, mm, kk, nn, rows=1)
+        res[f"{mm}x{kk}x{nn}"] = {"full_step_s": round(r["full_step_s"], 1), "tflops": round(r["tflops"], 6),
+                                  "sample": f"1-row slices, {r['sample_s']:.2f} s"}
+    return {"cores": 1, "kind": "port", "shapes": res}
+
+
+def _cpu_deep_mlp(O, np):
+    """The 4096-8192-8192-8192-4096-1000 MLP at batch 16384 on the oracle,
+    layer by layer on one-row slices (the first layer without dX, as on the
+    GPU); the full step's time is extrapolated (CE and SGD are O(M N), left
+    out)."""
+    dims, B = [4096, 8192, 8192, 8192, 4096, 1000], 16384
+    total, sample, layers = 0.0, 0.0, []
+    for l in range(len(dims) - 1):
+        r = _cpu_layer_slices(O, np, B, dims[l], dims[l + 1], rows=1)
+        # Remove the first layer's dX share (same cost as its forward share).
+        full = r["full_step_s"] * (2.0 / 3.0 if l == 0 else 1.0)
+        total += full
+        sample += r["sample_s"]
+        layers.append(round(full, 1))
+    macs = [B * dims[l] * dims[l + 1] for l in range(len(dims) - 1)]
+    flop = 6.0 * sum(macs) - 2.0 * macs[0]
+    return {"cores": 1, "kind": "port", "full_step_s": round(total, 1), "tflops": round(flop / total / 1e12, 6),
+            "per_layer_full_s": layers, "sample": f"1-row slices of every layer ({sample:.1f} s), extrapolated"}
+
+
+def _cpu_mlp(O, np, reps=20, warmup=3):
     """One full train step of the 784-256-128-10 MLP (batch 128) in the
-    oracle on one core: forward, softmax-CE, backward, SGD; median of reps."""
+    oracle on one core: forward, softmax-CE, backward, SGD; median of reps
+    after warm-up steps."""
     dims, B = [784, 256, 128, 10], 128
     X = O.uniform(1, (B, 784))
     Ws = [O.uniform(2 + l, (dims[l], dims[l + 1]), -(6.0 / dims[l]) ** 0.5, (6.0 / dims[l]) ** 0.5)
@@ -571,7 +684,7 @@ def _cpu_mlp(O, np, reps=5):
     bs = [np.zeros(dims[l + 1], np.float32) for l in range(3)]
     lbl = O.labels(9, B, 10)
     times = []
-    for _ in range(reps):
+    for it in range(warmup + reps):
         t0 = time.perf_counter()
         acts = [X]
         for l in range(3):
@@ -583,30 +696,51 @@ def _cpu_mlp(O, np, reps=5):
             g, dW, db = O.linear_bwd(acts[l], Ws[l], acts[l + 1], g, 1 if l < 2 else 0, want=want)
             O.sgd_update(Ws[l], dW, 1e-3)
             O.sgd_update(bs[l], db, 1e-3)
-        times.append(time.perf_counter() - t0)
+        if it >= warmup:
+            times.append(time.perf_counter() - t0)
     ms = sorted(times)[reps // 2] * 1e3
     macs = [B * dims[l] * dims[l + 1] for l in range(3)]
     flop = 6.0 * sum(macs) - 2.0 * macs[0]
     return {"ms_per_step": round(ms, 3), "tflops": round(flop / (ms * 1e-3) / 1e12, 6), "cores": 1,
-            "kind": "port", "sample": f"median of {reps} full steps"}
+            "kind": "port", "sample": f"median of {reps} full steps after {warmup} warm-up steps"}
 
 
-def _cpu_elementwise(O, np, n=1 << 24, reps=3):
-    """Oracle elementwise ops over 2^24 fp32 elements on one core (GB/s of
-    algorithmic traffic, median of reps)."""
-    a = O.normal(1, n)
-    b = O.uniform(2, n, 0.5, 2.0)
+def _cpu_elementwise(O, np):
+    """The eight oracle elementwise ops over 2^24 (median of 3) and 2^28 (one
+    run) fp32 elements on one core, GB/s of algorithmic traffic; relu-bwd
+    also split over min(cores, 8) threads (ctypes releases the GIL during
+    the oracle call, so the chunks run in parallel)."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    threads = min(os.cpu_count() or 1, 8)
     res = {}
-    for name, code in (("add", O.EW_ADD), ("div", O.EW_DIV), ("relu", O.EW_RELU), ("relu_bwd", O.EW_RELU_BWD)):
-        binary = code in O.EW_BINARY
-        times = []
-        for _ in range(reps):
-            t0 = time.perf_counter()
-            O.elementwise(code, a, b if binary else None, alpha=0.5)
-            times.append(time.perf_counter() - t0)
-        sec = sorted(times)[reps // 2]
-        res[name] = round((12 if binary else 8) * n / sec / 1e9, 2)
-    return {"GB/s": res, "cores": 1, "kind": "port", "sample": f"n = 2^24, median of {reps}"}
+    for log2n, reps in ((24, 3), (28, 1)):
+        n = 1 << log2n
+        a = _fill(np, n, 21)
+        b = np.abs(_fill(np, n, 22)) + np.float32(0.5)
+        ops = {}
+        for name, code in (("add", O.EW_ADD), ("sub", O.EW_SUB), ("mul", O.EW_MUL), ("div", O.EW_DIV),
+                           ("relu", O.EW_RELU), ("relu_bwd", O.EW_RELU_BWD), ("neg", O.EW_NEG),
+                           ("scale", O.EW_SCALE)):
+            binary = code in O.EW_BINARY
+            times = []
+            for _ in range(reps):
+                t0 = time.perf_counter()
+                O.elementwise(code, a, b if binary else None, alpha=0.5)
+                times.append(time.perf_counter() - t0)
+            ops[name] = round((12 if binary else 8) * n / sorted(times)[reps // 2] / 1e9, 2)
+        chunks = [(i * n // threads, (i + 1) * n // threads) for i in range(threads)]
+        with ThreadPoolExecutor(threads) as ex:
+            times = []
+            for _ in range(reps):
+                t0 = time.perf_counter()
+                list(ex.map(lambda c: O.elementwise(O.EW_RELU_BWD, a[c[0]:c[1]], b[c[0]:c[1]]), chunks))
+                times.append(time.perf_counter() - t0)
+        ops[f"relu_bwd_{threads}_threads"] = round(12 * n / sorted(times)[reps // 2] / 1e9, 2)
+        res[f"2^{log2n}"] = ops
+        del a, b
+    return {"GB/s": res, "cores": 1, "threads_relu_bwd": threads, "kind": "port",
+            "sample": "n = 2^24 median of 3, n = 2^28 one run"}
 
 
 def _cpu_model():

@@ -17,6 +17,7 @@
 
 #include <cstdio>
 #include <cstdlib>
+#include <algorithm>
 #include <cstring>
 #include <memory>
 #include <mutex>
@@ -29,6 +30,23 @@ namespace c3hip {
 namespace {
 
 thread_local std::string t_error;
+
+// Launch timing (c3hip_set_launch_timing): each launch of the thread between
+// two events on its stream.
+struct TimedLaunch {
+    std::string name;
+    hipEvent_t start = nullptr, stop = nullptr;
+};
+thread_local bool t_timing = false;
+thread_local std::vector<TimedLaunch> t_launches;
+
+void drop_timings() {
+    for (auto& t : t_launches) {
+        if (t.start) (void)hipEventDestroy(t.start);
+        if (t.stop) (void)hipEventDestroy(t.stop);
+    }
+    t_launches.clear();
+}
 
 struct DeviceState {
     int device = -1;
@@ -208,11 +226,62 @@ int launch(const char* name, dim3 grid, dim3 block, void** args, hipStream_t str
     hipFunction_t fn = nullptr;
     int rc = get_function(name, &fn);
     if (rc) return rc;
+    TimedLaunch tl;
+    if (t_timing) {
+        if (hipEventCreate(&tl.start) != hipSuccess || hipEventCreate(&tl.stop) != hipSuccess ||
+            hipEventRecord(tl.start, stream) != hipSuccess) {
+            (void)hipGetLastError();
+            if (tl.start) (void)hipEventDestroy(tl.start);
+            if (tl.stop) (void)hipEventDestroy(tl.stop);
+            return set_error(C3HIP_ERR_HIP, std::string("launch timing: event set-up failed for ") + name);
+        }
+    }
     hipError_t e = hipModuleLaunchKernel(fn, grid.x, grid.y, grid.z, block.x, block.y, block.z, 0, stream, args,
                                          nullptr);
+    if (t_timing) {
+        if (e == hipSuccess && hipEventRecord(tl.stop, stream) == hipSuccess) {
+            tl.name = name;
+            t_launches.push_back(tl);
+        } else {
+            (void)hipEventDestroy(tl.start);
+            (void)hipEventDestroy(tl.stop);
+        }
+    }
     if (e != hipSuccess)
         return set_error(C3HIP_ERR_HIP, std::string("hipModuleLaunchKernel(") + name + ") failed: " + hipGetErrorString(e));
     return C3HIP_OK;
+}
+
+int set_launch_timing(int enable) {
+    if (!enable) drop_timings();
+    t_timing = enable != 0;
+    return C3HIP_OK;
+}
+
+int launch_timings(char* names, size_t name_len, float* ms, int max, int* count) {
+    if (!count || max < 0 || (max > 0 && (!ms || (names && name_len == 0))))
+        return set_error(C3HIP_ERR_INVALID, "launch_timings: bad output buffers");
+    int n = 0;
+    int rc = C3HIP_OK;
+    for (auto& t : t_launches) {
+        if (n >= max) break;
+        float v = -1.0f;
+        if (hipEventSynchronize(t.stop) != hipSuccess || hipEventElapsedTime(&v, t.start, t.stop) != hipSuccess) {
+            (void)hipGetLastError();
+            rc = set_error(C3HIP_ERR_HIP, "launch timing: reading the events of " + t.name + " failed");
+            v = -1.0f;
+        }
+        ms[n] = v;
+        if (names) {
+            const size_t k = std::min(name_len - 1, t.name.size());
+            std::memcpy(names + (size_t)n * name_len, t.name.data(), k);
+            names[(size_t)n * name_len + k] = 0;
+        }
+        ++n;
+    }
+    drop_timings();
+    *count = n;
+    return rc;
 }
 
 int init_device(int device) {
@@ -309,6 +378,16 @@ int c3hip_load_code_object(const char* module_name, const void* image, size_t nb
 int c3hip_code_object_path(const char* module_name, char* buf, size_t buflen) {
     c3hip::clear_error();
     return c3hip::code_object_path(module_name, buf, buflen);
+}
+
+int c3hip_set_launch_timing(int enable) {
+    c3hip::clear_error();
+    return c3hip::set_launch_timing(enable);
+}
+
+int c3hip_launch_timings(char* names, size_t name_len, float* ms, int max, int* count) {
+    c3hip::clear_error();
+    return c3hip::launch_timings(names, name_len, ms, max, count);
 }
 
 }  // extern "C"

@@ -44,6 +44,9 @@ SIGNATURES = {
     "c3hip_shutdown": (_int, []),
     "c3hip_load_code_object": (_int, [ctypes.c_char_p, _vp, ctypes.c_size_t]),
     "c3hip_code_object_path": (_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_size_t]),
+    "c3hip_set_launch_timing": (_int, [_int]),
+    "c3hip_launch_timings": (_int, [ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(_f), _int,
+                                    ctypes.POINTER(_int)]),
     "c3hip_elementwise": (_int, [_int, _int, _vp, _vp, _f, _vp, _i64, _i64, _vp]),
     "c3hip_elementwise3": (_int, [_int, _int, _vp, _vp, _vp, _vp, _i64, _vp]),
     "c3hip_set_gemm_tile": (_int, [_int, ctypes.c_char_p]),
@@ -112,6 +115,21 @@ def init(device: int = 0) -> None:
 
 def shutdown() -> None:
     _check("c3hip_shutdown", load().c3hip_shutdown())
+
+
+def set_launch_timing(enable: bool) -> None:
+    """Bracket every kernel this thread launches through the library with HIP events."""
+    _check("c3hip_set_launch_timing", load().c3hip_set_launch_timing(int(enable)))
+
+
+def launch_timings(max_records: int = 65536, name_len: int = 96) -> list[tuple[str, float]]:
+    """(kernel name, ms) of each launch recorded since the last call, in launch order; clears them."""
+    names = ctypes.create_string_buffer(max_records * name_len)
+    ms = (_f * max_records)()
+    cnt = _int()
+    _check("c3hip_launch_timings", load().c3hip_launch_timings(names, name_len, ms, max_records, ctypes.byref(cnt)))
+    raw = names.raw
+    return [(raw[i * name_len:(i + 1) * name_len].split(b"\0", 1)[0].decode(), ms[i]) for i in range(cnt.value)]
 
 
 def elementwise(op: int, dtype: int, a: int, b: int | None, alpha: float, out: int, n: int, bmod: int = 0,

@@ -119,6 +119,22 @@ int c3hip_load_code_object(const char* module_name, const void* image, size_t nb
 int c3hip_code_object_path(const char* module_name, char* buf, size_t buflen);
 
 /*
+ * Per-launch timing, for measurement.  While enabled (enable != 0) on the
+ * calling thread, every kernel this library launches for that thread is
+ * bracketed by two HIP events recorded on the launch's stream; enable == 0
+ * stops it and drops unread records.  c3hip_launch_timings waits for the
+ * recorded launches and writes, in launch order, up to `max` records: the
+ * kernel name into names + i * name_len (NUL-terminated, truncated to
+ * name_len - 1; names may be NULL) and its duration between the two events
+ * in ms into ms[i]; *count receives the number written and all records are
+ * cleared.  The reference times its host-side calls with the host clock
+ * (C3KernelRegistry::recordPerf*, include/C3/C3KernelRegistry.h:256-275);
+ * device kernels are timed on the device here.
+ */
+int c3hip_set_launch_timing(int enable);
+int c3hip_launch_timings(char* names, size_t name_len, float* ms, int max, int* count);
+
+/*
  * Elementwise op over n contiguous elements: out[i] = op(a[li], b[ri]).
  * bmod > 0: ri = i mod bmod (rhs broadcast, e.g. a bias row); bmod < 0:
  * li = i mod -bmod (lhs broadcast); 0: no broadcast.  b is ignored (may be
