@@ -5,6 +5,8 @@ Products, all in-tree under c3_amd/lib/ (git-ignored, shipped with the tree):
   libc3hip.so    host C-ABI library (include/c3hip.h) that loads them
   libc3core.so   C++ dispatch layer (registry, hot-path manager, JIT cache)
   c3core_tests   C++ unit-test runner for the dispatch layer (CPU only)
+  san/c3core_tests_{tsan,asan}  the same tests with the dispatch layer built
+                 under ThreadSanitizer / AddressSanitizer (host code)
 and the oracle (test infrastructure) under oracle/liboracle.so.
 
 Run:  python -m c3_amd.build   (or __graft_entry__.build()).
@@ -96,6 +98,30 @@ def build_core_tests() -> Path:
     return out
 
 
+SANITIZERS = {"tsan": ["-Xarch_host", "-fsanitize=thread"],
+              "asan": ["-Xarch_host", "-fsanitize=address", "-fno-omit-frame-pointer"]}
+
+
+def build_sanitized_tests() -> list[Path]:
+    """tests/cpp/san/c3core_tests_{tsan,asan}: the dispatch layer's sources and
+    its unit tests in one executable, host code built with ThreadSanitizer or
+    AddressSanitizer (device code is not instrumented; the CPU tests launch
+    none)."""
+    out_dir = TESTS_CPP / "san"
+    out_dir.mkdir(parents=True, exist_ok=True)
+    srcs = [str(CSRC / "host" / "src" / s) for s in HOST_SOURCES]
+    jobs = []
+    for name, flags in SANITIZERS.items():
+        out = out_dir / f"c3core_tests_{name}"
+        jobs.append(([HIPCC, "-O1", "-g", "-std=c++17", *flags, f"-I{CSRC / 'host' / 'include'}", f"-I{INCLUDE}",
+                      f"-I{TESTS_CPP}", f"-I{ORACLE}", str(TESTS_CPP / "test_c3core.cpp"), *srcs, "-o", str(out),
+                      f"-L{LIB}", "-lc3hip", f"-L{ORACLE}", "-loracle", "-Wl,-rpath,$ORIGIN/../../../c3_amd/lib",
+                      "-Wl,-rpath,$ORIGIN/../../../oracle", "-lpthread"], out))
+    with ThreadPoolExecutor(max_workers=len(jobs)) as ex:
+        list(ex.map(lambda j: _run(j[0]), jobs))
+    return [j[1] for j in jobs]
+
+
 def build_oracle() -> Path:
     _run(["make", "-s", "-C", str(ORACLE), "liboracle.so"])
     return ORACLE / "liboracle.so"
@@ -108,6 +134,7 @@ def build_all(verbose: bool = False) -> None:
     built.append(build_core())
     built.append(build_oracle())
     built.append(build_core_tests())
+    built += build_sanitized_tests()
     if verbose:
         for b in built:
             print(f"built {b.relative_to(ROOT)} ({b.stat().st_size} bytes)")

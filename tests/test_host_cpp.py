@@ -50,3 +50,22 @@ def test_cpp_gpu(name, tmp_path):
     if not torch.cuda.is_available():
         pytest.skip("no GPU visible")
     _run(name, tmp_path)
+
+
+@pytest.mark.parametrize("san", ["tsan", "asan"])
+def test_cpu_tests_under_sanitizer(san, tmp_path):
+    """Every CPU C++ test, with the dispatch layer (registry, hot-path
+    manager's background compiles, backward capture, JIT cache, caching pool)
+    built under ThreadSanitizer or AddressSanitizer: all pass and the
+    sanitizer reports nothing."""
+    exe = ROOT / "tests" / "cpp" / "san" / f"c3core_tests_{san}"
+    assert exe.exists(), f"{exe} is not built: run __graft_entry__.build()"
+    env = dict(os.environ)
+    env["C3_AOT_CACHE_DIR"] = str(tmp_path)
+    env["TSAN_OPTIONS"] = "halt_on_error=1 second_deadlock_stack=1"
+    env["ASAN_OPTIONS"] = "halt_on_error=1 detect_leaks=1"
+    p = subprocess.run([str(exe)], capture_output=True, text=True, timeout=600, env=env)
+    out = p.stdout + p.stderr
+    assert "Sanitizer" not in out, out[-4000:]
+    assert p.returncode == 0, out[-4000:]
+    assert out.count("PASS ") == len(CPU_NAMES), out[-2000:]
