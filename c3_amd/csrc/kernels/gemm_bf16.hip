@@ -366,6 +366,37 @@ struct DirectTile {
         }
     }
 
+    // A last k-tile holding only kr < BK valid k (kr a multiple of 8 for KC
+    // operands, any for RC ones): lanes whose 16-byte chunk lies below kr
+    // issue their DMA as issue() does; the others write zeros to the LDS slot
+    // their DMA would fill, so the fragments past kr are exact zeros and
+    // nothing beyond the operand is read.  Used only by 2-stage kernels, whose
+    // tile waits are vmcnt(0), so a wave that skips its DMA instructions does
+    // not upset the wait counts.
+    __device__ __forceinline__ void issue_partial(const unsigned short* P, unsigned short* S, int wave, int lane,
+                                                  int kr) const {
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int q = wave * NI + i;
+            // KC: the lane's global chunk is its LDS slot XOR the row's key
+            // (see init); RC: its k-row.
+            const int kc_row = (64 / KC_CPR) * q + lane / KC_CPR;
+            const bool valid = KC ? (8 * ((lane % KC_CPR) ^ kc_key(kc_row)) < kr)
+                                  : (q * (64 / RC_CPR) + lane / RC_CPR < kr);
+            unsigned short* slot = S + q * 512;
+            if (valid) {
+                const uint32_t lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)slot;
+                const unsigned short* src = P + goff[i];
+                asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+                             :
+                             : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(src)
+                             : "memory", "m0");
+            } else {
+                *(u32x4*)(slot + 8 * lane) = u32x4{0u, 0u, 0u, 0u};
+            }
+        }
+    }
+
     // The i-th of this wave's NI DMA instructions (same effect as issue() for
     // that instruction alone), so the issue can be spread between MFMAs.
     __device__ __forceinline__ void issue_one(const unsigned short* P, unsigned short* S, int wave, int i) const {
@@ -572,24 +603,28 @@ __device__ __forceinline__ void gemm_bf16_direct_body(const GemmArgs& p) {
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-    const int nk = (int)(p.K / BK);
-#pragma unroll
-    for (int t = 0; t < PF; ++t) {
-        if (t < nk) {
-            unsigned short* S = smem + t * STAGE;
+    // k-tiles; the last one holds kr_last valid k (BK when K % BK == 0; only
+    // 2-stage kernels are launched with K % BK != 0).
+    const int nk = (int)((p.K + BK - 1) / BK);
+    const int kr_last = (int)(p.K - (int64_t)(nk - 1) * BK);
+    auto issue_tile = [&](int t, unsigned short* S) {
+        if (STAGES == 2 && t == nk - 1 && kr_last < BK) {
+            la.issue_partial(A + (int64_t)t * a_kstep, S, wave, lane, kr_last);
+            lb.issue_partial(B + (int64_t)t * b_kstep, S + A_EL, wave, lane, kr_last);
+        } else {
             la.issue(A + (int64_t)t * a_kstep, S, wave);
             lb.issue(B + (int64_t)t * b_kstep, S + A_EL, wave);
         }
+    };
+#pragma unroll
+    for (int t = 0; t < PF; ++t) {
+        if (t < nk) issue_tile(t, smem + t * STAGE);
     }
 
     for (int kt = 0; kt < nk; ++kt) {
         wait_tiles_after<NIW, PF>(min(nk - 1 - kt, PF - 1));
         __syncthreads();
-        if (kt + PF < nk) {
-            unsigned short* S = smem + ((kt + PF) % STAGES) * STAGE;
-            la.issue(A + (int64_t)(kt + PF) * a_kstep, S, wave);
-            lb.issue(B + (int64_t)(kt + PF) * b_kstep, S + A_EL, wave);
-        }
+        if (kt + PF < nk) issue_tile(kt + PF, smem + ((kt + PF) % STAGES) * STAGE);
         const unsigned short* As = smem + (kt % STAGES) * STAGE;
         const unsigned short* Bs = As + A_EL;
 #pragma unroll

@@ -64,7 +64,8 @@ const char* kind_name(Kind k) {
 struct Tile {
     const char* name;
     int bm, bn, threads;
-    int bk;  // k depth of one tile (direct-to-LDS kernels: K must be a multiple); 0 = any K
+    int bk;             // k depth of one tile (direct-to-LDS kernels); 0 = any K
+    bool ktail = false;  // direct kernel takes a partial last k-tile (else K must be a multiple of bk)
 };
 
 // Threads per block of the vector elementwise and backward-chain kernels
@@ -131,14 +132,19 @@ const Tile* choose_bf16_tile(int64_t M, int64_t N) {
 // backward masks are applied by the pre-pass), K a multiple of the tile's k
 // depth, and a problem of at least 64 output tiles so the large tile fills
 // the chip.
-const Tile kBf16Direct[] = {{"d256w8", 256, 256, 512, 64},
-                             {"d256rq", 256, 256, 256, 64},
-                             {"d256pp", 256, 256, 512, 32},
-                             {"d128w4", 128, 128, 256, 64}};
+const Tile kBf16Direct[] = {{"d256w8", 256, 256, 512, 64, true},
+                             {"d256rq", 256, 256, 256, 64, false},
+                             {"d256pp", 256, 256, 512, 32, false},
+                             {"d128w4", 128, 128, 256, 64, true}};
+
+// K a multiple of the tile's k depth, or any K for a tile with a partial
+// last k-tile (whose k-contiguous operands have K % 8 == 0 by the 16-byte
+// vector rule checked before).
+bool k_ok(const GemmArgs& a, const Tile* t) { return a.K % t->bk == 0 || t->ktail; }
 
 bool direct_eligible(Kind kind, const GemmArgs& a, const Tile* t) {
     if (kind == Kind::DxMask || kind == Kind::DwMask || a.db != nullptr) return false;
-    return a.K > 0 && a.M >= 8 && a.N >= 8 && a.K % t->bk == 0;
+    return a.K > 0 && a.M >= 8 && a.N >= 8 && k_ok(a, t);
 }
 
 int64_t tile_count(const GemmArgs& a, const Tile* t) { return ((a.M + t->bm - 1) / t->bm) * ((a.N + t->bn - 1) / t->bn); }
@@ -194,7 +200,7 @@ const Tile* choose_bf16_direct(Kind kind, const GemmArgs& a, bool* unsupported, 
     if (a.M < 8 || a.N < 8) return nullptr;
     const Tile* big = find_tile(kBf16Direct, nd, "d256w8");
     const Tile* small = find_tile(kBf16Direct, nd, "d128w4");
-    if (a.K % big->bk != 0) return nullptr;
+    if (!k_ok(a, big) || !k_ok(a, small)) return nullptr;
     if (tile_count(a, big) >= 256) return big;
     const int64_t tiles_s = tile_count(a, small);
     const int Ss = tiles_s >= 256 ? 1 : plan_split(a, small, 512, 512);  // 256 blocks: one per CU already

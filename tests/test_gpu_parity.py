@@ -349,6 +349,31 @@ def test_every_bf16_tile_bit_exact(gpu, stream, monkeypatch, tile):
     same_bits(host(db), rb)
 
 
+@pytest.mark.parametrize("tile", [None, "d256w8", "d128w4"])
+@pytest.mark.parametrize("M,K,Nn", [(328, 1000, 264), (301, 1000, 264), (200, 72, 136), (264, 40, 8)])
+def test_bf16_direct_k_tail_bit_exact(gpu, stream, monkeypatch, tile, M, K, Nn):
+    # k extents that are not multiples of the direct kernels' 64-deep k-tile:
+    # forward k = K, dX k = N, dW k = M (any M; the others multiples of 8).
+    # The last tile loads only its valid chunks and zero-fills the rest.
+    from tests.parity import dev_bf16
+
+    if tile:
+        monkeypatch.setenv("C3_HIP_GEMM_TILE_BF16", tile)
+    X, W, b, dY = ints(91, (M, K)), ints(92, (K, Nn)), ints(93, Nn), ints(94, (M, Nn))
+    Y = empty((M, Nn), dtype=torch.bfloat16)
+    N.linear_fwd(N.BF16, ptr(dev_bf16(X)), ptr(dev_bf16(W)), ptr(dev(b)), ptr(Y), M, K, Nn, 1, stream)
+    rY = _bf16_round(O.linear_fwd(X, W, b, 1))
+    same_bits(host(Y), rY)
+    dX = empty((M, K), dtype=torch.bfloat16)
+    dW, db = empty((K, Nn)), empty(Nn)
+    N.linear_bwd(N.BF16, ptr(dev_bf16(X)), ptr(dev_bf16(W)), ptr(Y), ptr(dev_bf16(dY)), ptr(dX), ptr(dW), ptr(db),
+                 M, K, Nn, 1, stream)
+    rX, rW, rb = O.linear_bwd(X, W, rY, dY, 1)
+    same_bits(host(dX), _bf16_round(rX))
+    same_bits(host(dW), rW)
+    same_bits(host(db), rb)
+
+
 @pytest.mark.parametrize("M,K,Nn", BF16_SHAPES)
 def test_bf16_real(gpu, stream, M, K, Nn):
     from tests.parity import dev_bf16
@@ -421,7 +446,9 @@ def test_forced_tile_override(gpu, stream):
             N.set_gemm_tile(N.BF16, tile)
             Y = empty((M, Nn), dtype=torch.bfloat16)
             args = (N.BF16, ptr(dev_bf16(X)), ptr(dev_bf16(W)), ptr(dev(b)), ptr(Y), M, K, Nn, 1, stream)
-            if tile.startswith("d"):  # direct tiles: K = 264 is not a multiple of their 32/64-deep k tile
+            # K = 264 is not a multiple of the direct tiles' 32/64-deep k tile: those
+            # with a partial last k-tile run it, the others refuse it.
+            if tile.startswith("d") and tile not in ("d256w8", "d128w4"):
                 with pytest.raises(N.C3HipError) as e:
                     N.linear_fwd(*args)
                 assert e.value.code == N.ERR_UNSUPPORTED
