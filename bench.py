@@ -54,6 +54,10 @@ def parse():
                     help="only run the bf16 forward GEMM (c3hip_linear_fwd, bias + ReLU) and torch.matmul "
                          "(hipBLASLt) alternately at 8192x4096x4096 and 16384x8192x8192 on random data, for "
                          "rocprofv3 kernel-trace and MFMA-busy/clock counter summaries of both")
+    ap.add_argument("--bf16-gemm-kinds", action="store_true",
+                    help="only run the three bf16 GEMMs of a Linear layer (forward with bias + ReLU, dX, dW) at "
+                         "16384x8192x8192 on the size heuristic's kernels, 10 launches each, for rocprofv3 "
+                         "counter summaries of the bf16 GEMM kernels")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain copy-like stream (scale: read 2^26 fp32, write 2^26 fp32) three times; "
                          "its FETCH_SIZE/WRITE_SIZE counters calibrate the HBM traffic figures")
@@ -98,6 +102,38 @@ def elementwise_profile(log2n=28, sets=1, reps=3):
     torch.cuda.synchronize()
     print(json.dumps({"elementwise_profile": {"n": n, "operand_sets": sets, "launches_per_op": reps * sets,
                                               "ops": list(C.EW_OPS)}}), flush=True)
+
+
+def bf16_gemm_kinds(m=16384, k=8192, n=8192, reps=10):
+    """The forward (bias + ReLU), dX and dW GEMMs of a bf16 Linear layer,
+    each `reps` times, through c3hip_linear_fwd / c3hip_linear_bwd (dX alone,
+    dW alone, no activation: each call is exactly one GEMM launch)."""
+    import torch
+
+    from c3_amd import native as C
+
+    C.init(0)
+    dev = torch.device("cuda:0")
+    s = torch.cuda.current_stream().cuda_stream
+    g = torch.Generator(device=dev)
+    g.manual_seed(0xB1A6)
+    X = torch.randn(m, k, device=dev, generator=g).to(torch.bfloat16)
+    W = (torch.randn(k, n, device=dev, generator=g) / float(k) ** 0.5).to(torch.bfloat16)
+    b = torch.randn(n, device=dev, generator=g) * 0.1
+    dZ = torch.randn(m, n, device=dev, generator=g).to(torch.bfloat16)
+    Y = torch.empty(m, n, device=dev, dtype=torch.bfloat16)
+    dX = torch.empty(m, k, device=dev, dtype=torch.bfloat16)
+    dW = torch.empty(k, n, device=dev)
+    for _ in range(reps):
+        C.linear_fwd(C.BF16, X.data_ptr(), W.data_ptr(), b.data_ptr(), Y.data_ptr(), m, k, n, C.ACT_RELU, s)
+    for _ in range(reps):
+        C.linear_bwd(C.BF16, None, W.data_ptr(), None, dZ.data_ptr(), dX.data_ptr(), None, None, m, k, n,
+                     C.ACT_NONE, s)
+    for _ in range(reps):
+        C.linear_bwd(C.BF16, X.data_ptr(), None, None, dZ.data_ptr(), None, dW.data_ptr(), None, m, k, n,
+                     C.ACT_NONE, s)
+    torch.cuda.synchronize()
+    print(json.dumps({"bf16_gemm_kinds": {"shape": f"{m}x{k}x{n}", "launches_per_kind": reps}}), flush=True)
 
 
 def gemm_compare(reps=10, rounds=3):
@@ -162,6 +198,9 @@ def main():
         return
     if args.gemm_compare:
         gemm_compare()
+        return
+    if args.bf16_gemm_kinds:
+        bf16_gemm_kinds()
         return
 
     import torch

@@ -9,6 +9,7 @@
 // MatMul+ReLU: saved 0 (never active).
 #pragma once
 
+#include <algorithm>
 #include <cstddef>
 #include <vector>
 
@@ -31,24 +32,27 @@ public:
 
     static bool isComputeIntensive(op op_type) { return op_type == op::MatMul; }
 
+    // Element accesses of the sequence run op by op (every output written,
+    // every output but the last read back by its consumer) and what one
+    // fused kernel saves (the write and the read of each intermediate that
+    // is not compute-intensive).  Only the first min(|op_seq|, |out_numels|)
+    // ops count.  With I = the intermediates and L = the last output:
+    //   eager = L + 2 * sum(I),  saved = 2 * sum(I that are not MatMul).
     static FusionCost estimate(const std::vector<op>& op_seq, const std::vector<size_t>& out_numels) {
-        FusionCost cost;
-        const size_t n = op_seq.size() < out_numels.size() ? op_seq.size() : out_numels.size();
-        if (n == 0) return cost;
-        size_t write_all = 0, read_intermediate = 0;
-        for (size_t i = 0; i < n; ++i) {
-            write_all += out_numels[i];
-            if (i + 1 < n) read_intermediate += out_numels[i];
+        FusionCost c;
+        const size_t count = std::min(op_seq.size(), out_numels.size());
+        if (count == 0) return c;
+        size_t intermediates = 0, removable = 0;
+        for (size_t k = 0; k + 1 < count; ++k) {
+            intermediates += out_numels[k];
+            if (!isComputeIntensive(op_seq[k])) removable += out_numels[k];
         }
-        cost.eager_accesses = write_all + read_intermediate;
-        for (size_t i = 0; i + 1 < n; ++i)
-            if (!isComputeIntensive(op_seq[i])) cost.saved_accesses += out_numels[i] * 2;
-        cost.fused_accesses =
-            cost.eager_accesses > cost.saved_accesses ? cost.eager_accesses - cost.saved_accesses : 0;
-        if (cost.eager_accesses > 0)
-            cost.gain_ratio = static_cast<double>(cost.saved_accesses) / static_cast<double>(cost.eager_accesses);
-        cost.worthwhile = cost.saved_accesses > 0 && cost.gain_ratio >= kMinGainRatio;
-        return cost;
+        c.eager_accesses = out_numels[count - 1] + 2 * intermediates;
+        c.saved_accesses = 2 * removable;
+        c.fused_accesses = c.eager_accesses - c.saved_accesses;  // saved <= eager by construction
+        c.gain_ratio = c.eager_accesses ? (double)c.saved_accesses / (double)c.eager_accesses : 0.0;
+        c.worthwhile = c.saved_accesses > 0 && c.gain_ratio >= kMinGainRatio;
+        return c;
     }
 };
 

@@ -263,6 +263,15 @@ TEST(cost_model_closed_forms) {
     auto e = FusionCostModel::estimate({op::Add, op::ReLU, op::Neg}, {10, 10, 10});
     CHECK(std::fabs(e.gain_ratio - 0.8) < 1e-12);
     CHECK(FusionCostModel::estimate({}, {}).eager_accesses == 0);
+    CHECK_EQ(c.fused_accesses, 3 * mn);
+    // Lengths differ: only the common prefix counts (MatMul, Add over [mn] -> eager 3mn, saved 0).
+    auto f = FusionCostModel::estimate({op::MatMul, op::Add, op::ReLU}, {mn, mn});
+    CHECK_EQ(f.eager_accesses, 3 * mn);
+    CHECK_EQ(f.saved_accesses, (size_t)0);
+    CHECK(!f.worthwhile);
+    // Empty outputs: no accesses, ratio 0, not worthwhile.
+    auto z = FusionCostModel::estimate({op::Add, op::ReLU}, {0, 0});
+    CHECK(z.eager_accesses == 0 && z.gain_ratio == 0.0 && !z.worthwhile);
 }
 
 TEST(sha256_fips_vectors) {
