@@ -150,6 +150,79 @@ extern "C" __global__ __launch_bounds__(kThreads) void c3_dz_colsum_f32(
     }
 }
 
+// fp32, vectorised: one thread owns 4 consecutive columns (a 16-byte vector);
+// block = vb vectors x (256 / vb) row lanes, grid (ceil(N / 4 / vb), nchunks).
+// Each column's rows are summed in the same order as in c3_dz_colsum_f32 run
+// on the same row geometry.  Requires N % 4 == 0 and 16-byte aligned rows.
+extern "C" __global__ __launch_bounds__(kThreads) void c3_dz_colsum_f32_v(
+    const float* __restrict__ Y, const float* __restrict__ dY, float* __restrict__ dZ, float* __restrict__ part,
+    int64_t M, int64_t N, int64_t rows_per_chunk, int act, int vb) {
+    __shared__ float red[kThreads][5];
+    const int rb = kThreads / vb;
+    const int u = threadIdx.x % vb, rl = threadIdx.x / vb;
+    const int64_t v = (int64_t)blockIdx.x * vb + u;  // vector index within a row
+    const bool active = 4 * v < N;
+    const int64_t chunk = blockIdx.y;
+    const int64_t r0 = chunk * rows_per_chunk;
+    const int64_t r1 = min(M, r0 + rows_per_chunk);
+    float s[4] = {0.f, 0.f, 0.f, 0.f};
+    auto grad = [&](f32x4 y, f32x4 d) {
+        return f32x4{act_grad(y[0], d[0], act), act_grad(y[1], d[1], act), act_grad(y[2], d[2], act),
+                     act_grad(y[3], d[3], act)};
+    };
+    if (active) {
+        // Four rows per iteration, their loads issued before the first use;
+        // rows are still summed in row order.
+        const bool need_y = act != 0;
+        int64_t i = r0 + rl;
+        for (; i + 3 * rb < r1; i += 4 * rb) {
+            f32x4 d[4], y[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int64_t off = (i + q * rb) * N + 4 * v;
+                d[q] = __builtin_nontemporal_load((const f32x4*)(dY + off));
+                y[q] = need_y ? __builtin_nontemporal_load((const f32x4*)(Y + off)) : f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int64_t off = (i + q * rb) * N + 4 * v;
+                const f32x4 g = grad(y[q], d[q]);
+                if (dZ) *(f32x4*)(dZ + off) = g;
+                if (part) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) s[e] += g[e];
+                }
+            }
+        }
+        for (; i < r1; i += rb) {
+            const int64_t off = i * N + 4 * v;
+            const f32x4 d = __builtin_nontemporal_load((const f32x4*)(dY + off));
+            const f32x4 y = need_y ? __builtin_nontemporal_load((const f32x4*)(Y + off)) : f32x4{0.f, 0.f, 0.f, 0.f};
+            const f32x4 g = grad(y, d);
+            if (dZ) *(f32x4*)(dZ + off) = g;
+            if (part) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) s[e] += g[e];
+            }
+        }
+    }
+    if (part) {
+        if (rb > 1) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) red[threadIdx.x][e] = s[e];
+            __syncthreads();
+            if (rl == 0)
+                for (int k = 1; k < rb; ++k)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) s[e] += red[threadIdx.x + k * vb][e];
+        }
+        if (rl == 0 && active) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) part[chunk * N + 4 * v + e] = s[e];
+        }
+    }
+}
+
 // bf16: one thread owns 8 consecutive columns (a 16-byte vector); block = vb
 // vectors x (256 / vb) row lanes, grid (ceil(N / 8 / vb), nchunks).  ReLU
 // works on the bit patterns (exact); sigmoid and tanh compute in fp32 and

@@ -72,8 +72,12 @@ struct Tile {
 // (elementwise.hip kVecThreads): one float4 per thread.
 constexpr int64_t kEwVecThreads = 64;
 
-const Tile kF32Tiles[] = {{"t64x64", 64, 64, 256}, {"t128x128", 128, 128, 256}, {"t256x128", 256, 128, 512},
-                          {"t128x256", 128, 256, 512}};
+// The last two are the direct-to-LDS twins (gemm_f32.hip, names ending in d) of the
+// register-staged 256x128 and 128x256 tiles: same blocks and bits, taken for
+// unmasked GEMMs with K % 16 == 0 (f32_direct).
+const Tile kF32Tiles[] = {{"t64x64", 64, 64, 256},        {"t128x128", 128, 128, 256}, {"t256x128", 256, 128, 512},
+                          {"t128x256", 128, 256, 512},    {"t256x128d", 256, 128, 512, 16},
+                          {"t128x256d", 128, 256, 512, 16}};
 const Tile kBf16Tiles[] = {{"t64x64", 64, 64, 256},
                            {"t128x128", 128, 128, 256},
                            {"t256x128", 256, 128, 256},
@@ -112,6 +116,23 @@ const Tile* choose_f32_tile(Kind kind, int64_t M, int64_t N) {
     const int64_t blocks128 = ((M + 127) / 128) * ((N + 127) / 128);
     if (blocks128 >= 512) return &kF32Tiles[1];
     return &kF32Tiles[0];
+}
+
+// Direct-to-LDS twin of register tile t for GEMM `kind`, or null.  The
+// direct kernels take the plain forward, dX and dW (with or without the db
+// side output): no masked operand, no dZ side output, K a multiple of 16 and
+// vector-aligned operands (vec).  Measured on MI355X at 8192x4096x4096,
+// alternating with the register kernels in one process (bit-identical
+// outputs): forward 132.5 -> 139.0 TFLOP/s, dX 133 -> 138.5 (its first
+// fragment reads issued before the next tile's DMA), dW with db 128.5 ->
+// 134.6, without db 138.7.
+const Tile* f32_direct(Kind kind, const GemmArgs& a, const Tile* t, bool vec) {
+    if (t->bk) t = t->bm == 256 ? &kF32Tiles[2] : &kF32Tiles[3];  // forced twin: decide as for its register tile
+    const bool plain = kind == Kind::Fwd || kind == Kind::Dx || kind == Kind::Dw;
+    if (!plain || a.Amask || a.Bmask || a.dz || !vec || a.K < 16 || a.K % 16 != 0) return nullptr;
+    if (t == &kF32Tiles[2]) return &kF32Tiles[4];
+    if (t == &kF32Tiles[3]) return &kF32Tiles[5];
+    return nullptr;
 }
 
 const char* bf16_forced() {
@@ -388,6 +409,19 @@ int run_gemm(int dtype, Kind kind, const GemmArgs& a0, bool a_kc, bool b_kc, hip
     }
     const Tile* t = choose_f32_tile(kind, a.M, a.N);
     const bool vec = vec_ok(a_kc, a.M, a.K, a.lda, a.A, a.Amask) && vec_ok(b_kc, a.N, a.K, a.ldb, a.B, a.Bmask);
+    // A forced register tile runs as itself; the size heuristic's big tiles
+    // and a forced direct tile run direct where f32_direct allows (else the
+    // direct tile's register twin).
+    const bool forced_reg = f32_forced() && !t->bk;
+    if (const Tile* d = forced_reg ? nullptr : f32_direct(kind, a, t, vec)) {
+        char name[96];
+        std::snprintf(name, sizeof(name), "c3_gemm_f32_%s_%s", kind_name(kind), d->name);
+        const int64_t blocks = tile_count(a, d);
+        if (blocks > 0x7fffffff) return set_error(C3HIP_ERR_TOO_LARGE, "GEMM grid too large");
+        void* args[] = {&a};
+        return launch(name, dim3((unsigned)blocks), dim3(d->threads), args, stream);
+    }
+    if (t->bk) t = t->bm == 256 ? &kF32Tiles[2] : &kF32Tiles[3];
     if (const int S = plan_split_f32(a, t)) return run_split_f32(kind, a, t, S, vec, stream, ws);
     char name[96];
     std::snprintf(name, sizeof(name), "c3_gemm_f32_%s_%s_%s", kind_name(kind), t->name, vec ? "v" : "s");
@@ -500,9 +534,10 @@ int colsum(const float* in, const float* mask, float* out, int64_t M, int64_t N,
 // Backward through a pre-pass: one pass forms dZ = act'(Y) * dY (in the
 // layer's dtype, stream-ordered workspace) together with the per-chunk column
 // sums for db, then dX and dW run as plain GEMMs on dZ.  Used for every bf16
-// backward (the direct-to-LDS kernels cannot apply a mask while loading) and
-// for the fp32 sigmoid/tanh backward (the fp32 GEMMs fuse only the ReLU
-// mask).  Without an activation, dZ is dY itself.
+// backward (the direct-to-LDS kernels cannot apply a mask while loading), for
+// the fp32 sigmoid/tanh backward (the fp32 GEMMs fuse only the ReLU mask), and
+// for the fp32 ReLU backward whose plain dX and dW run direct (f32_bwd_direct).
+// Without an activation, dZ is dY itself.
 int linear_bwd_prepass(int dtype, const void* X, const void* W, const void* Y, const void* dY, void* dX, float* dW,
                        float* db, int64_t M, int64_t K, int64_t N, int act, hipStream_t stream) {
     const size_t esz = dtype == C3HIP_BF16 ? 2 : 4;
@@ -524,7 +559,9 @@ int linear_bwd_prepass(int dtype, const void* X, const void* W, const void* Y, c
     if (dtype == C3HIP_BF16 && (N % 8 != 0 || !aligned16(Y) || !aligned16(dY)))
         return set_error(C3HIP_ERR_UNSUPPORTED, "bf16 backward needs N % 8 == 0 and 16-byte aligned Y, dY");
     const bool need_dz = act != C3HIP_ACT_NONE && (dX || dW);
-    const ColGeom g = col_geom(M, dtype == C3HIP_BF16 ? N / 8 : N);
+    // fp32 rows of 16-byte vectors take the vector pre-pass (4 columns per thread).
+    const bool f32v = dtype == C3HIP_F32 && N % 4 == 0 && aligned16(Y) && aligned16(dY);
+    const ColGeom g = col_geom(M, dtype == C3HIP_BF16 ? N / 8 : f32v ? N / 4 : N);
     int64_t nchunks = g.nchunks, rows_per_chunk = g.rows_per_chunk;
     int vb = g.vb;
     void* dz = nullptr;
@@ -541,8 +578,8 @@ int linear_bwd_prepass(int dtype, const void* X, const void* W, const void* Y, c
         float* part_out = db ? (nchunks > 1 ? part : db) : nullptr;
         int act_i = act;
         void* args[] = {(void*)&Y, (void*)&dY, &dz, &part_out, &M, &N, &rows_per_chunk, &act_i, &vb};
-        rc = launch(dtype == C3HIP_BF16 ? "c3_dz_colsum_bf16" : "c3_dz_colsum_f32", dim3(g.gx, (unsigned)nchunks),
-                    dim3(256), args, stream);
+        rc = launch(dtype == C3HIP_BF16 ? "c3_dz_colsum_bf16" : f32v ? "c3_dz_colsum_f32_v" : "c3_dz_colsum_f32",
+                    dim3(g.gx, (unsigned)nchunks), dim3(256), args, stream);
         if (rc == C3HIP_OK && db && nchunks > 1) rc = colsum_final(part, db, nchunks, N, stream);
     }
     const void* dzp = need_dz ? dz : dY;
@@ -741,6 +778,26 @@ int c3hip_linear_fwd(int dtype, const void* X, const void* W, const float* b, vo
     return c3hip::linear_fwd(dtype, X, W, b, Y, M, K, N, act, (hipStream_t)stream, nullptr);
 }
 
+// fp32 ReLU backward through the vector pre-pass (dZ and the db partials in
+// one stream over dY and Y) and plain direct-to-LDS dX and dW on dZ, when both
+// plain GEMMs of this shape would run direct: measured on MI355X at
+// 8192x4096x4096 the three launches take 65 + 1985 + 1980 us against 2165 +
+// 2146 us for the masked dX that writes dZ and dW + db on it.  Decided on the
+// shape and alignment alone, not on which of dX, dW, db are asked for, so a
+// call for a subset of them returns the bits of the full call (db is then
+// always the pre-pass column sum).
+bool f32_bwd_direct(const GemmArgs& ax, const GemmArgs& aw, const void* Y, const void* dY) {
+    if (ax.K % 4 != 0 || !aligned16(Y) || !aligned16(dY)) return false;
+    const auto direct = [](Kind kind, GemmArgs a, bool a_kc, bool b_kc) {
+        a.Amask = a.Bmask = nullptr;
+        a.db = nullptr;
+        const bool vec = vec_ok(a_kc, a.M, a.K, a.lda, a.A, nullptr) && vec_ok(b_kc, a.N, a.K, a.ldb, a.B, nullptr);
+        if (f32_forced() && !choose_f32_tile(kind, a.M, a.N)->bk) return false;
+        return f32_direct(kind, a, choose_f32_tile(kind, a.M, a.N), vec) != nullptr;
+    };
+    return direct(Kind::Dx, ax, true, true) && direct(Kind::Dw, aw, false, false);
+}
+
 // Both GEMMs of a small fp32 layer backward in one launch (c3_gemm_f32_bwd*):
 // taken when each would run as a plain 64x64-tile launch (no split-K, no
 // forced tile) and the two grids hold at most 128 tiles together, where a
@@ -796,6 +853,8 @@ int c3hip_linear_bwd(int dtype, const void* X, const void* W, const void* Y, con
         if (rc != C3HIP_ERR_UNSUPPORTED) return rc;  // launched (or failed); unsupported: separate launches
         clear_error();
     }
+    if (relu && M > 0 && N > 0 && K > 0 && f32_bwd_direct(ax, aw, Y, dY))
+        return linear_bwd_prepass(dtype, X, W, Y, dY, dX, dW, db, M, K, N, act, stream);
     if (relu && dX && dW && M > 0 && N > 0 && K > 0) {
         // Both GEMMs: dX forms dZ = mask(Y) * dY in its operand loads anyway,
         // so it also writes dZ (each k-tile once, from the staging registers)

@@ -962,7 +962,7 @@ TEST(merged_kernel_runs_layers_in_order) {
 }
 
 // A PGO kernel: eager first (the interpreter) and the compile chain; then
-// the Ofast tuner times the four fp32 tiles on real calls (the host kernels
+// the Ofast tuner times the six fp32 tiles on real calls (the host kernels
 // sleep per tile, t128x128 fastest) and keeps the fastest; results are the
 // same on every tier.
 TEST(pgo_tiers_tune_and_deopt) {
@@ -972,7 +972,12 @@ TEST(pgo_tiers_tune_and_deopt) {
     E.setFactoryForTest([](const KernelSpec& sp, const CompileOptions& o) -> std::shared_ptr<CompiledKernel> {
         g_built++;
         auto inner = std::make_shared<HostKernel>(sp, o.opt_level);
-        const int ms = sp.tile == "t64x64" ? 4 : sp.tile == "t256x128" ? 8 : sp.tile == "t128x256" ? 6 : 0;
+        const int ms = sp.tile == "t64x64"      ? 4
+                       : sp.tile == "t256x128"  ? 8
+                       : sp.tile == "t128x256"  ? 6
+                       : sp.tile == "t256x128d" ? 7
+                       : sp.tile == "t128x256d" ? 5
+                                                : 0;
         return std::make_shared<ScriptedKernel>(o.opt_level, [inner, ms](const std::vector<Tensor>& in) {
             if (ms) std::this_thread::sleep_for(std::chrono::milliseconds(ms));
             return inner->execute(in);
@@ -991,14 +996,14 @@ TEST(pgo_tiers_tune_and_deopt) {
     CHECK_EQ(rig.interpreted.load(), 1);
     CHECK(k->isPromoted() && k->o2Kernel() && k->ofastKernel());
     auto tuners = k->tuners();
-    CHECK(tuners.size() == 1 && tuners[0] && tuners[0]->candidateCount() == 4);
+    CHECK(tuners.size() == 1 && tuners[0] && tuners[0]->candidateCount() == 6);
     int calls = 1;
     while (!tuners[0]->tuned() && calls < 40) {
         CHECK(vals(k->execute(in)[0]) == want);
         ++calls;
     }
     CHECK(tuners[0]->tuned());
-    CHECK_EQ(calls, 1 + 4 * (1 + P.config().tune_samples));
+    CHECK_EQ(calls, 1 + 6 * (1 + P.config().tune_samples));
     CHECK_EQ(tuners[0]->chosen(), std::string("t128x128"));
     CHECK(vals(k->execute(in)[0]) == want);
     CHECK_EQ(rig.interpreted.load(), 1);
@@ -1054,7 +1059,8 @@ TEST(pgo_backpressure_queue_and_merged_plan) {
     CHECK(vals(k->execute(in)[0]) == want);  // Ofast merged: both layers' tuners
     auto tuners = k->tuners();
     CHECK(tuners.size() == 2 && tuners[0] && tuners[1]);
-    for (int i = 0; i < 20; ++i) CHECK(vals(k->execute(in)[0]) == want);
+    const int n_tiles = (int)tuners[0]->candidateCount();
+    for (int i = 0; i < n_tiles * (1 + P.config().tune_samples) + 1; ++i) CHECK(vals(k->execute(in)[0]) == want);
     CHECK(tuners[0]->tuned() && tuners[1]->tuned());
     CHECK_EQ(rig.interpreted.load(), 2);
     // promoteAll on a fresh kernel compiles it in the calling thread.

@@ -52,13 +52,16 @@ def test_code_objects_hold_every_dispatched_kernel():
         for tile in ["t64x64", "t128x128", "t256x128", "t128x256"]:
             for v in "vs":
                 assert f"c3_gemm_f32_{kind}_{tile}_{v}" in gemm
+    for kind in ["fwd", "dx", "dw"]:
+        for tile in ["t256x128d", "t128x256d"]:
+            assert f"c3_gemm_f32_{kind}_{tile}" in gemm
     for name in ["c3_gemm_f32_bwd_t64x64", "c3_gemm_f32_bwd_mask_t64x64"]:
         assert f"{name}_v" in gemm and f"{name}_s" in gemm
     ew = _kernel_symbols(LIB / "elementwise.hsaco")
     for op in list(native.EW_OPS) + list(native.EW_MATH_OPS):
         assert f"c3_ew_{op}_f32_v" in ew and f"c3_ew_{op}_f32_s" in ew
     assert "c3_ew3_div_bwd_b_f32" in ew
-    assert {"c3_dz_colsum_f32", "c3_dz_colsum_bf16"} <= _kernel_symbols(LIB / "reduce.hsaco")
+    assert {"c3_dz_colsum_f32", "c3_dz_colsum_f32_v", "c3_dz_colsum_bf16"} <= _kernel_symbols(LIB / "reduce.hsaco")
     red = _kernel_symbols(LIB / "reduce.hsaco")
     assert {"c3_colsum_partial_f32", "c3_colsum_final_f32", "c3_rowsum_f32"} <= red
     loss = _kernel_symbols(LIB / "loss.hsaco")
@@ -132,7 +135,7 @@ def test_backward_chain_validation():
 
 
 def test_gemm_tile_override_validation():
-    assert native.gemm_tile_names(native.F32) == ["t64x64", "t128x128", "t256x128", "t128x256"]
+    assert native.gemm_tile_names(native.F32) == ["t64x64", "t128x128", "t256x128", "t128x256", "t256x128d", "t128x256d"]
     assert native.gemm_tile_names(native.BF16) == ["t64x64", "t128x128", "t256x128", "t256x256", "d256w8", "d256rq", "d256pp", "d128w4"]
     L = native.load()
     assert L.c3hip_set_gemm_tile(native.F32, b"d256w8") == native.ERR_INVALID  # a bf16-only tile

@@ -170,8 +170,8 @@ def test_small_bwd_one_launch_matches_two(gpu, stream, monkeypatch, M, K, Nn, ac
     assert_close_gemm(one[1], rW, gemm_bound(X.T, O.relu_mask_mul(Y, dY) if act else dY, M), FP32_TOL, what="dW")
 
 
-@pytest.mark.parametrize("tile", ["t64x64", "t128x128", "t256x128", "t128x256"])
-@pytest.mark.parametrize("M,K,Nn", [(300, 260, 200), (257, 128, 64)])
+@pytest.mark.parametrize("tile", ["t64x64", "t128x128", "t256x128", "t128x256", "t256x128d", "t128x256d"])
+@pytest.mark.parametrize("M,K,Nn", [(300, 260, 200), (257, 128, 64), (272, 144, 80)])
 def test_every_fp32_tile_bit_exact(gpu, stream, monkeypatch, tile, M, K, Nn):
     # Each tile the planner can pick, forced for every GEMM of the layer
     # (forward, dX with mask, dW with mask and db), on ragged extents.
@@ -188,7 +188,7 @@ def test_every_fp32_tile_bit_exact(gpu, stream, monkeypatch, tile, M, K, Nn):
     same_bits(gb, rb)
 
 
-@pytest.mark.parametrize("tile", [None, "t64x64", "t128x128", "t256x128", "t128x256"])
+@pytest.mark.parametrize("tile", [None, "t64x64", "t128x128", "t256x128", "t128x256", "t256x128d", "t128x256d"])
 @pytest.mark.parametrize("M,K,Nn", [(1024, 768, 1536), (300, 260, 200), (2048, 1024, 4096)])
 def test_bwd_dz_side_output_matches_masked_launches(gpu, stream, monkeypatch, tile, M, K, Nn):
     # With dX and dW both asked for, the dX kernel also writes dZ = mask(Y) dY
@@ -208,6 +208,36 @@ def test_bwd_dz_side_output_matches_masked_launches(gpu, stream, monkeypatch, ti
     same_bits(both[0], gx)
     same_bits(both[1], gw)
     same_bits(both[2], gb)
+
+
+@pytest.mark.parametrize("pair", [("t256x128d", "t256x128"), ("t128x256d", "t128x256")])
+@pytest.mark.parametrize("M,K,Nn", [(512, 256, 384), (1000, 512, 776), (272, 144, 80), (300, 272, 200)])
+def test_f32_direct_tiles_match_register_tiles(gpu, stream, monkeypatch, pair, M, K, Nn):
+    # The direct-to-LDS tiles (operands DMA'd into LDS, three stages) multiply
+    # in the register tiles' order, so the forward, dX and dW agree bit for bit
+    # on real-valued inputs, ragged extents included.  With K, N and M all
+    # multiples of 16 the direct backward runs through the dZ pre-pass, whose
+    # db sums in another order than the dW kernel's side output: db within the
+    # fp32 bound of both against the oracle.
+    X = O.normal(91, (M, K))
+    W = O.normal(92, (K, Nn), 0.0, 1.0 / np.sqrt(K))
+    b = O.normal(93, Nn, 0.0, 0.1)
+    dY = O.normal(94, (M, Nn))
+    outs = {}
+    for tile in pair:
+        monkeypatch.setenv("C3_HIP_GEMM_TILE", tile)
+        Yg = empty((M, Nn))
+        N.linear_fwd(N.F32, ptr(dev(X)), ptr(dev(W)), ptr(dev(b)), ptr(Yg), M, K, Nn, 1, stream)
+        Y = host(Yg)
+        outs[tile] = (Y,) + _run_bwd(stream, X, W, Y, dY, 1)
+    d, r = outs[pair[0]], outs[pair[1]]
+    for i, name in enumerate(("Y", "dX", "dW")):
+        same_bits(d[i], r[i])
+    Y = d[0]
+    rb = O.linear_bwd(X, W, Y, dY, 1)[2]
+    bound = 2.02 * M * 2.0 ** -24 * np.abs(O.relu_mask_mul(Y, dY).astype(np.float64)).sum(0)
+    for gb in (d[3], r[3]):
+        assert_close_gemm(gb, rb, bound, FP32_TOL, what="db")
 
 
 @pytest.mark.parametrize("M,K,Nn", BWD_SHAPES)
