@@ -58,6 +58,9 @@ def parse():
                     help="only run the three bf16 GEMMs of a Linear layer (forward with bias + ReLU, dX, dW) at "
                          "16384x8192x8192 on the size heuristic's kernels, 10 launches each, for rocprofv3 "
                          "counter summaries of the bf16 GEMM kernels")
+    ap.add_argument("--bf16-sweep-only", action="store_true",
+                    help="only run the bf16 M x K x N sweep (one JSON line), for a rocprofv3 kernel trace "
+                         "summarised per shape")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain copy-like stream (scale: read 2^26 fp32, write 2^26 fp32) three times; "
                          "its FETCH_SIZE/WRITE_SIZE counters calibrate the HBM traffic figures")
@@ -210,6 +213,9 @@ def main():
     C.init(0)
     dev = torch.device("cuda:0")
     stream = torch.cuda.current_stream()
+    if args.bf16_sweep_only:
+        print(json.dumps({"bf16_sweep": bench_bf16_sweep(torch, C, dev, stream.cuda_stream)}), flush=True)
+        return
     s = stream.cuda_stream
     g = torch.Generator(device=dev)
     g.manual_seed(0xC3)
@@ -230,8 +236,9 @@ def main():
                      db.data_ptr(), M, K, N, C.ACT_RELU, s)
 
     # A step is c3hip_linear_fwd + c3hip_linear_bwd (dX, dW, db): the forward
-    # GEMM, then the dX GEMM (which also writes dZ) and the dW + db GEMM on dZ.
-    # Each launch is timed on its stream by the library's launch timing.
+    # GEMM, then the backward's dZ = mask(Y) dY pass (with the db partials and
+    # their final sum) and the dX and dW GEMMs on dZ.  Each launch is timed on
+    # its stream by the library's launch timing.
     def step():
         fwd()
         bwd()
@@ -244,7 +251,7 @@ def main():
     wall_tflops = flop_step * args.steps / wall / 1e12
     per_kernel_ms = {k: v["avg_ms"] for k, v in kt.items()}
 
-    # Each of the three GEMMs does 2 M N K flop per launch.
+    # Each of the three GEMMs does 2 M N K flop per launch; the slowest is the dominant kernel.
     dom = max(per_kernel_ms, key=per_kernel_ms.get)
     dom_ms = per_kernel_ms[dom]
     dom_achieved = 2.0 * M * N * K / (dom_ms * 1e-3) / 1e12

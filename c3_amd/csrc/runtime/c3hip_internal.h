@@ -29,6 +29,16 @@ int launch(const char* name, dim3 grid, dim3 block, void** args, hipStream_t str
 int set_launch_timing(int enable);
 int launch_timings(char* names, size_t name_len, float* ms, int max, int* count);
 
+// Workspace of one call (split-K partials, dZ, column-sum partials, W^T):
+// carved from the library's arena for (current device, stream) when the
+// stream is not being captured and no other thread is using that arena,
+// else hipMallocAsync on the stream.  *arena says which; ws_free takes it
+// back.  The arena is reset when the last workspace of the call is freed
+// (the stream orders the next call's kernels after this one's) and grown,
+// after synchronizing the stream, when a call needed more than it held.
+int ws_alloc(size_t bytes, hipStream_t stream, void** p, bool* arena, const char* what);
+int ws_free(void* p, bool arena, hipStream_t stream, const char* what);
+
 // Kernel argument block of every GEMM code object (mirrors GemmArgs in
 // c3_amd/csrc/kernels/gemm_common.h; both sides are plain C layout).
 struct GemmArgs {

@@ -232,11 +232,15 @@ const Tile* choose_bf16_direct(Kind kind, const GemmArgs& a, bool* unsupported, 
     return nullptr;
 }
 
+// Where a call's workspace came from: the caller's (nothing to free), the
+// library's arena for the stream, or the stream-ordered allocator.
+enum class WsHow { Caller, Arena, Stream };
+
 // A workspace of `bytes` for one call: from ws when it has a base (capacity
-// checked, nothing launched on failure), else from the stream-ordered pool;
-// *owned tells release_workspace to free it.
-int take_workspace(const Workspace* ws, size_t bytes, hipStream_t stream, void** p, bool* owned, const char* what) {
-    *owned = false;
+// checked, nothing launched on failure), else from ws_alloc; *how tells
+// release_workspace how to give it back.
+int take_workspace(const Workspace* ws, size_t bytes, hipStream_t stream, void** p, WsHow* how, const char* what) {
+    *how = WsHow::Caller;
     if (ws && ws->base) {
         if (bytes > ws->bytes)
             return set_error(C3HIP_ERR_TOO_LARGE, std::string(what) + " needs " + std::to_string(bytes) +
@@ -245,22 +249,21 @@ int take_workspace(const Workspace* ws, size_t bytes, hipStream_t stream, void**
         *p = ws->base;
         return C3HIP_OK;
     }
-    hipError_t e = hipMallocAsync(p, bytes, stream);
-    if (e != hipSuccess) return set_error(C3HIP_ERR_HIP, std::string("hipMallocAsync(") + what + "): " + hipGetErrorString(e));
-    *owned = true;
+    bool arena = false;
+    const int rc = ws_alloc(bytes, stream, p, &arena, what);
+    if (rc) return rc;
+    *how = arena ? WsHow::Arena : WsHow::Stream;
     return C3HIP_OK;
 }
 
-int release_workspace(void* p, bool owned, int rc, hipStream_t stream, const char* what) {
-    if (!owned) return rc;
-    hipError_t e = hipFreeAsync(p, stream);
-    if (rc == C3HIP_OK && e != hipSuccess)
-        rc = set_error(C3HIP_ERR_HIP, std::string("hipFreeAsync(") + what + "): " + hipGetErrorString(e));
-    return rc;
+int release_workspace(void* p, WsHow how, int rc, hipStream_t stream, const char* what) {
+    if (how == WsHow::Caller) return rc;
+    const int frc = ws_free(p, how == WsHow::Arena, stream, what);
+    return rc != C3HIP_OK ? rc : frc;
 }
 
 // Split-K run of a plain bf16 GEMM on direct tile d: S block rows write fp32
-// partial products into a stream-ordered workspace [S, M, N]; the reduction
+// partial products into a workspace of the call [S, M, N]; the reduction
 // adds them in split order and applies the kind's epilogue (forward: bias and
 // activation, bf16 out; dW: fp32 out; the others: bf16 out).
 int run_split(Kind kind, const GemmArgs& a0, const Tile* d, int S, hipStream_t stream, const Workspace* wsp) {
@@ -271,9 +274,9 @@ int run_split(Kind kind, const GemmArgs& a0, const Tile* d, int S, hipStream_t s
                                                                 : "dw";
     const bool fwd = kind == Kind::Fwd || kind == Kind::FwdT;
     float* ws = nullptr;
-    bool owned = false;
+    WsHow how;
     const int64_t slice = a0.M * a0.N;
-    int rc = take_workspace(wsp, (size_t)S * (size_t)slice * sizeof(float), stream, (void**)&ws, &owned, "split-K");
+    int rc = take_workspace(wsp, (size_t)S * (size_t)slice * sizeof(float), stream, (void**)&ws, &how, "split-K");
     if (rc) return rc;
     GemmArgs g = a0;
     g.C = ws;
@@ -303,7 +306,7 @@ int run_split(Kind kind, const GemmArgs& a0, const Tile* d, int S, hipStream_t s
         void* rargs[] = {&r};
         rc = launch("c3_splitk_reduce", dim3((unsigned)((threads + 255) / 256)), dim3(256), rargs, stream);
     }
-    return release_workspace(ws, owned, rc, stream, "split-K");
+    return release_workspace(ws, how, rc, stream, "split-K");
 }
 
 // bf16 kernels always move 16-byte vectors (8 elements): the contiguous
@@ -342,8 +345,8 @@ int run_split_f32(Kind kind, const GemmArgs& a0, const Tile* t, int S, bool vec,
     S = (int)((a0.K + split_k - 1) / split_k);
     const int64_t slice = a0.M * a0.N;
     float* ws = nullptr;
-    bool owned = false;
-    int rc = take_workspace(wsp, (size_t)S * (size_t)slice * sizeof(float), stream, (void**)&ws, &owned, "split-K");
+    WsHow how;
+    int rc = take_workspace(wsp, (size_t)S * (size_t)slice * sizeof(float), stream, (void**)&ws, &how, "split-K");
     if (rc) return rc;
     GemmArgs g = a0;
     g.C = ws;
@@ -372,7 +375,7 @@ int run_split_f32(Kind kind, const GemmArgs& a0, const Tile* t, int S, bool vec,
         void* rargs[] = {&r};
         rc = launch("c3_splitk_reduce", dim3((unsigned)((threads + 255) / 256)), dim3(256), rargs, stream);
     }
-    return release_workspace(ws, owned, rc, stream, "split-K");
+    return release_workspace(ws, how, rc, stream, "split-K");
 }
 
 int run_gemm(int dtype, Kind kind, const GemmArgs& a0, bool a_kc, bool b_kc, hipStream_t stream,
@@ -450,8 +453,8 @@ bool bf16_fwd_transposed(const GemmArgs& a) {
 
 int linear_fwd_wt(const GemmArgs& a0, hipStream_t stream) {
     void* wt = nullptr;
-    hipError_t e = hipMallocAsync(&wt, (size_t)(a0.K * a0.N) * 2, stream);
-    if (e != hipSuccess) return set_error(C3HIP_ERR_HIP, std::string("hipMallocAsync(W^T): ") + hipGetErrorString(e));
+    WsHow how;
+    if (int rc0 = take_workspace(nullptr, (size_t)(a0.K * a0.N) * 2, stream, &wt, &how, "W^T")) return rc0;
     const void* w = a0.B;
     int64_t R = a0.K, Cc = a0.N;
     void* targs[] = {(void*)&w, &wt, &R, &Cc};
@@ -463,10 +466,7 @@ int linear_fwd_wt(const GemmArgs& a0, hipStream_t stream) {
         a.ldb = a0.K;
         rc = run_gemm(C3HIP_BF16, Kind::FwdT, a, true, true, stream);
     }
-    e = hipFreeAsync(wt, stream);
-    if (rc == C3HIP_OK && e != hipSuccess)
-        rc = set_error(C3HIP_ERR_HIP, std::string("hipFreeAsync(W^T): ") + hipGetErrorString(e));
-    return rc;
+    return release_workspace(wt, how, rc, stream, "W^T");
 }
 
 int check_elems(const char* what, int64_t rows, int64_t cols) {
@@ -508,7 +508,7 @@ int colsum_final(const float* part, float* out, int64_t nchunks, int64_t N, hipS
 }
 
 // Column sums of (optionally masked) fp32 [M,N] into out[N]: one pass when
-// one chunk covers M, else per-chunk partials in a stream-ordered workspace.
+// one chunk covers M, else per-chunk partials in a workspace of the call.
 int colsum(const float* in, const float* mask, float* out, int64_t M, int64_t N, hipStream_t stream) {
     if (N == 0) return C3HIP_OK;
     ColGeom g = col_geom(M, N);
@@ -520,19 +520,18 @@ int colsum(const float* in, const float* mask, float* out, int64_t M, int64_t N,
         return launch(pname, dim3(g.gx, 1), dim3(256), args, stream);
     }
     float* part = nullptr;
-    hipError_t e = hipMallocAsync((void**)&part, (size_t)(nchunks * N) * sizeof(float), stream);
-    if (e != hipSuccess) return set_error(C3HIP_ERR_HIP, std::string("hipMallocAsync failed: ") + hipGetErrorString(e));
+    WsHow how;
+    if (int rc0 = take_workspace(nullptr, (size_t)(nchunks * N) * sizeof(float), stream, (void**)&part, &how,
+                                 "column-sum partials"))
+        return rc0;
     void* args1[] = {(void*)&in, (void*)&mask, (void*)&part, &M, &N, &rows_per_chunk, &vb};
     int rc = launch(pname, dim3(g.gx, (unsigned)nchunks), dim3(256), args1, stream);
     if (rc == C3HIP_OK) rc = colsum_final(part, out, nchunks, N, stream);
-    e = hipFreeAsync(part, stream);
-    if (rc == C3HIP_OK && e != hipSuccess)
-        rc = set_error(C3HIP_ERR_HIP, std::string("hipFreeAsync failed: ") + hipGetErrorString(e));
-    return rc;
+    return release_workspace(part, how, rc, stream, "column-sum partials");
 }
 
 // Backward through a pre-pass: one pass forms dZ = act'(Y) * dY (in the
-// layer's dtype, stream-ordered workspace) together with the per-chunk column
+// layer's dtype, a workspace of the call) together with the per-chunk column
 // sums for db, then dX and dW run as plain GEMMs on dZ.  Used for every bf16
 // backward (the direct-to-LDS kernels cannot apply a mask while loading), for
 // the fp32 sigmoid/tanh backward (the fp32 GEMMs fuse only the ReLU mask), and
@@ -566,13 +565,14 @@ int linear_bwd_prepass(int dtype, const void* X, const void* W, const void* Y, c
     int vb = g.vb;
     void* dz = nullptr;
     float* part = nullptr;
+    WsHow dz_how = WsHow::Caller, part_how = WsHow::Caller;
     int rc = C3HIP_OK;
-    hipError_t e;
-    if (need_dz && (e = hipMallocAsync(&dz, (size_t)(M * N) * esz, stream)) != hipSuccess)
-        return set_error(C3HIP_ERR_HIP, std::string("hipMallocAsync(dZ): ") + hipGetErrorString(e));
-    if (db && nchunks > 1 && (e = hipMallocAsync((void**)&part, (size_t)(nchunks * N) * sizeof(float), stream)) != hipSuccess) {
-        if (dz) (void)hipFreeAsync(dz, stream);
-        return set_error(C3HIP_ERR_HIP, std::string("hipMallocAsync(partials): ") + hipGetErrorString(e));
+    if (need_dz && (rc = take_workspace(nullptr, (size_t)(M * N) * esz, stream, &dz, &dz_how, "dZ"))) return rc;
+    if (db && nchunks > 1 &&
+        (rc = take_workspace(nullptr, (size_t)(nchunks * N) * sizeof(float), stream, (void**)&part, &part_how,
+                             "column-sum partials"))) {
+        if (dz) (void)release_workspace(dz, dz_how, rc, stream, "dZ");
+        return rc;
     }
     if (need_dz || db) {
         float* part_out = db ? (nchunks > 1 ? part : db) : nullptr;
@@ -597,8 +597,8 @@ int linear_bwd_prepass(int dtype, const void* X, const void* W, const void* Y, c
         a.lda = K; a.ldb = N; a.ldc = N;
         rc = run_gemm(dtype, Kind::Dw, a, false, false, stream);
     }
-    if (dz) (void)hipFreeAsync(dz, stream);
-    if (part) (void)hipFreeAsync(part, stream);
+    if (part) rc = release_workspace(part, part_how, rc, stream, "column-sum partials");
+    if (dz) rc = release_workspace(dz, dz_how, rc, stream, "dZ");
     return rc;
 }
 
@@ -863,8 +863,8 @@ int c3hip_linear_bwd(int dtype, const void* X, const void* W, const void* Y, con
         // are the same IEEE operations, so every output has the bits of the
         // masked launches.  Without memory for dZ, the masked launches run.
         void* dz = nullptr;
-        bool owned = false;
-        if (take_workspace(nullptr, (size_t)(M * N) * sizeof(float), stream, &dz, &owned, "dZ") == C3HIP_OK) {
+        WsHow how;
+        if (take_workspace(nullptr, (size_t)(M * N) * sizeof(float), stream, &dz, &how, "dZ") == C3HIP_OK) {
             GemmArgs a1 = ax;
             a1.dz = dz;
             rc = run_gemm(dtype, Kind::DxMaskDz, a1, true, true, stream);
@@ -874,7 +874,7 @@ int c3hip_linear_bwd(int dtype, const void* X, const void* W, const void* Y, con
                 a2.Bmask = nullptr;
                 rc = run_gemm(dtype, Kind::Dw, a2, false, false, stream);
             }
-            return release_workspace(dz, owned, rc, stream, "dZ");
+            return release_workspace(dz, how, rc, stream, "dZ");
         }
         clear_error();
     }
