@@ -197,7 +197,9 @@ int forced_split(const GemmArgs& a, const Tile* t) {
 // Sets *unsupported when the calling thread forced a direct tile this
 // problem cannot use; *split receives the split-K factor (1: none).
 // Size heuristic (measured on MI355X over the 1024..16384 sweep shapes):
-//  - 256x256 tiles when they give at least 256 blocks (one per CU);
+//  - 256x256 tiles when they give at least 256 blocks (one per CU), or, for
+//    a weight gradient, reach 256 blocks with k split into parts at least
+//    4096 deep;
 //  - else 128x128 tiles when they give at least 128 blocks, or for K >= 2048
 //    when split-K brings them there; below 256 blocks the k range is split
 //    into parts at least 512 deep, up to 512 blocks (two per CU);
@@ -222,7 +224,24 @@ const Tile* choose_bf16_direct(Kind kind, const GemmArgs& a, bool* unsupported, 
     const Tile* big = find_tile(kBf16Direct, nd, "d256w8");
     const Tile* small = find_tile(kBf16Direct, nd, "d128w4");
     if (!k_ok(a, big) || !k_ok(a, small)) return nullptr;
-    if (tile_count(a, big) >= 256) return big;
+    const int64_t tiles_b = tile_count(a, big);
+    if (tiles_b >= 256) return big;
+    // A weight gradient (k = the batch) on too few 256x256 tiles: split k
+    // into parts at least 4096 deep until the splits fill the chip with one
+    // block per CU.  Measured on MI355X for dW of the 4096 -> 1000 layer at
+    // batch 16384: d128w4 on its 256 tiles (one block per CU) 229.5 us.
+    // (Forward and dX keep the plans below, whose fp32 partials stay within
+    // the no-allocation entry point's scratch.)
+    if ((kind == Kind::Dw || kind == Kind::DwB) && tiles_b >= 32 && a.K >= 2 * 4096) {
+        int S = 1;
+        while (tiles_b * S < 256 && a.K / (2 * S) >= 4096 && a.K % (2 * S * big->bk) == 0 &&
+               (double)(2 * S) * (double)a.M * (double)a.N * 4.0 <= (double)(256u << 20))
+            S *= 2;
+        if (tiles_b * S >= 256) {
+            *split = S;
+            return big;
+        }
+    }
     const int64_t tiles_s = tile_count(a, small);
     const int Ss = tiles_s >= 256 ? 1 : plan_split(a, small, 512, 512);  // 256 blocks: one per CU already
     if (tiles_s >= 128 || (a.K >= 2048 && tiles_s * Ss >= 128)) {
