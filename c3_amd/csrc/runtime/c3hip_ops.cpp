@@ -203,7 +203,9 @@ int forced_split(const GemmArgs& a, const Tile* t) {
 //  - else 128x128 tiles when they give at least 128 blocks, or for K >= 2048
 //    when split-K brings them there; below 256 blocks the k range is split
 //    into parts at least 512 deep, up to 512 blocks (two per CU);
-//  - else the register-staged kernels (best for a 1024^3-sized problem).
+//  - else, for a weight gradient, 128x128 tiles when splits at least 256
+//    deep reach 256 blocks;
+//  - else the register-staged kernels (best for a 1024^3-sized forward and dX).
 const Tile* choose_bf16_direct(Kind kind, const GemmArgs& a, bool* unsupported, int* split) {
     *unsupported = false;
     *split = 1;
@@ -247,6 +249,19 @@ const Tile* choose_bf16_direct(Kind kind, const GemmArgs& a, bool* unsupported, 
     if (tiles_s >= 128 || (a.K >= 2048 && tiles_s * Ss >= 128)) {
         *split = Ss;
         return small;
+    }
+    // A weight gradient below that: 128x128 tiles with k split into parts at
+    // least 256 deep when that reaches 256 blocks, where the register-staged
+    // kernels read both (row-contiguous) operands slowly.  Measured on MI355X
+    // at 1024x1024x1024: 18.5 us (4 splits) against 26.0 for the 64x64
+    // register tile; the forward and dX stay on the register tiles (18.2 /
+    // 10.9 us against 19.3 / 18.4).
+    if (kind == Kind::Dw || kind == Kind::DwB) {
+        const int S = plan_split(a, small, 512, 256);
+        if (tiles_s * S >= 256) {
+            *split = S;
+            return small;
+        }
     }
     return nullptr;
 }
