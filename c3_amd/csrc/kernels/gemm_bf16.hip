@@ -587,9 +587,9 @@ __device__ __forceinline__ void store_tile_t(const GemmArgs& p, f32x16 (&acc)[FM
 // 8192x4096x4096 forward +7% (1026 -> 1096 TF/s), dX +1%, dW +0.3%; at
 // 16384x8192x8192 +2% / +3% / +0.5%.  Issuing the last k-step's MFMAs after
 // the next tile's barrier as well (so they cover that barrier) was 1-3% slower.
-template <int WAVES_M, int WAVES_N, bool AK, bool BKC, int EPI, int BK, int STAGES, int BT, bool EARLY = false>
+template <int WAVES_M, int WAVES_N, bool AK, bool BKC, int EPI, int BK, int STAGES, int BM, int BN, bool EARLY = false>
 __device__ __forceinline__ void gemm_bf16_direct_body(const GemmArgs& p) {
-    constexpr int BM = BT, BN = BT, NW = WAVES_M * WAVES_N;
+    constexpr int NW = WAVES_M * WAVES_N;
     constexpr int TM = BM / WAVES_M, TN = BN / WAVES_N, FM = TM / 32, FN = TN / 32;
     constexpr int PF = STAGES - 1;  // tiles in flight ahead of the one multiplied
     using TA = DirectTile<BM, AK, NW, BK>;
@@ -949,7 +949,7 @@ C3_GEMM_BF16_PP_KINDS(d256pp, 32, 4)
 #define C3_GEMM_BF16_D(NAME, WM, WN, AK, BKC, EPI, BK, ST, BT) C3_GEMM_BF16_DE(NAME, WM, WN, AK, BKC, EPI, BK, ST, BT, false)
 #define C3_GEMM_BF16_DE(NAME, WM, WN, AK, BKC, EPI, BK, ST, BT, E)                                 \
     extern "C" __global__ __launch_bounds__(64 * WM * WN) void NAME(GemmArgs p) {                 \
-        gemm_bf16_direct_body<WM, WN, AK, BKC, EPI, BK, ST, BT, E>(split_args<AK, BKC, EPI>(p));   \
+        gemm_bf16_direct_body<WM, WN, AK, BKC, EPI, BK, ST, BT, BT, E>(split_args<AK, BKC, EPI>(p)); \
     }
 
 // fwd: X (KC) . W (RC) + bias, act -> bf16.  fwdt: the same with W given
