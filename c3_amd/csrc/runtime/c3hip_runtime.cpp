@@ -354,10 +354,43 @@ struct Arena {
     size_t cap = 0, used = 0, want = 0;
     int live = 0;
     std::thread::id owner;
+    uint64_t last_use = 0;
 };
 std::mutex g_arena_mu;
 std::map<std::pair<int, hipStream_t>, Arena> g_arenas;
+uint64_t g_arena_clock = 0;
 constexpr size_t kArenaAlign = 256;
+// Arenas kept per device: a process that cycles through many streams (one
+// per request, say) would otherwise keep one per stream it ever used.  The
+// least recently used idle arena beyond this is freed after a device
+// synchronisation (its stream may no longer exist).
+constexpr int kMaxArenasPerDevice = 8;
+
+// The arena for (dev, stream), made if new; evicts as above.  The caller
+// holds g_arena_mu.
+Arena& arena_for(int dev, hipStream_t stream) {
+    auto it = g_arenas.find({dev, stream});
+    if (it == g_arenas.end()) {
+        int n = 0;
+        auto lru = g_arenas.end();
+        for (auto j = g_arenas.begin(); j != g_arenas.end(); ++j) {
+            if (j->first.first != dev) continue;
+            ++n;
+            if (j->second.live == 0 && (lru == g_arenas.end() || j->second.last_use < lru->second.last_use)) lru = j;
+        }
+        if (n >= kMaxArenasPerDevice && lru != g_arenas.end()) {
+            if (!lru->second.base)
+                g_arenas.erase(lru);
+            else if (hipDeviceSynchronize() == hipSuccess && hipFree(lru->second.base) == hipSuccess)
+                g_arenas.erase(lru);
+            else
+                (void)hipGetLastError();
+        }
+        it = g_arenas.emplace(std::make_pair(dev, stream), Arena{}).first;
+    }
+    it->second.last_use = ++g_arena_clock;
+    return it->second;
+}
 }  // namespace
 
 int ws_alloc(size_t bytes, hipStream_t stream, void** p, bool* arena, const char* what) {
@@ -374,7 +407,7 @@ int ws_alloc(size_t bytes, hipStream_t stream, void** p, bool* arena, const char
     int dev = 0;
     if (cs == hipStreamCaptureStatusNone && hipGetDevice(&dev) == hipSuccess) {
         std::lock_guard<std::mutex> lock(g_arena_mu);
-        Arena& a = g_arenas[{dev, stream}];
+        Arena& a = arena_for(dev, stream);
         if (a.live == 0 || a.owner == std::this_thread::get_id()) {
             const size_t off = (a.used + kArenaAlign - 1) / kArenaAlign * kArenaAlign;
             if (off + bytes <= a.cap) {

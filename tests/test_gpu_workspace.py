@@ -111,6 +111,20 @@ def test_arena_two_threads_on_one_stream(gpu, monkeypatch):
                 _same(_host(o), r)
 
 
+def test_arenas_of_many_streams_are_bounded(gpu, monkeypatch):
+    # More streams than the library keeps arenas for (8 per device): the least
+    # recently used idle arena is freed (after a device synchronisation) as
+    # each new stream arrives; every call still returns the reference bits.
+    shape = SHAPES[0]
+    problems = _problems(0x400, [shape])
+    streams = [torch.cuda.Stream() for _ in range(12)]
+    ref = _reference(monkeypatch, streams[0].cuda_stream, problems)
+    for rnd in range(2):
+        outs = [_bwd(st.cuda_stream, problems[0][0], *shape) for st in streams]
+        for o in outs:
+            _same(_host(o), ref[0])
+
+
 def test_arena_freed_by_shutdown_and_rebuilt(gpu, monkeypatch):
     s = torch.cuda.Stream()
     shape = SHAPES[1]
