@@ -657,3 +657,10 @@ __device__ __forceinline__ void gemm_f32_direct_body(const GemmArgs& p) {
 
 C3_GEMM_F32_D_KINDS(t256x128d, 256, 128, 4, 2)
 C3_GEMM_F32_D_KINDS(t128x256d, 128, 256, 2, 4)
+// 256x256: 8 waves of 128x64, one block per CU (98 KiB of LDS), half the
+// operand bytes per flop of the tiles above; taken for dX and dW on grids of
+// at least 256 such tiles (measured at 8192x4096x4096, alternating in one
+// process: dX 141.0 against 138.7 TFLOP/s, dW 139.6 against 138.7; the
+// forward is faster on 256x128, 139.2 against 137.9).
+C3_GEMM_F32_D(c3_gemm_f32_dx_t256x256d, 256, 256, 2, 4, true, true, false, true)
+C3_GEMM_F32_D(c3_gemm_f32_dw_t256x256d, 256, 256, 2, 4, false, false, true, false)

@@ -72,12 +72,14 @@ struct Tile {
 // (elementwise.hip kVecThreads): one float4 per thread.
 constexpr int64_t kEwVecThreads = 64;
 
-// The last two are the direct-to-LDS twins (gemm_f32.hip, names ending in d) of the
-// register-staged 256x128 and 128x256 tiles: same blocks and bits, taken for
-// unmasked GEMMs with K % 16 == 0 (f32_direct).
+// The last three are direct-to-LDS tiles (gemm_f32.hip, names ending in d):
+// the twins of the register-staged 256x128 and 128x256 tiles (same blocks and
+// bits) and a 256x256 tile for dX and dW, taken for unmasked GEMMs with
+// K % 16 == 0 (f32_direct).  Every fp32 tile multiplies each output's k range
+// in the same order, so all of them give the same bits.
 const Tile kF32Tiles[] = {{"t64x64", 64, 64, 256},        {"t128x128", 128, 128, 256}, {"t256x128", 256, 128, 512},
                           {"t128x256", 128, 256, 512},    {"t256x128d", 256, 128, 512, 16},
-                          {"t128x256d", 128, 256, 512, 16}};
+                          {"t128x256d", 128, 256, 512, 16}, {"t256x256d", 256, 256, 512, 16}};
 const Tile kBf16Tiles[] = {{"t64x64", 64, 64, 256},
                            {"t128x128", 128, 128, 256},
                            {"t256x128", 256, 128, 256},
@@ -118,6 +120,16 @@ const Tile* choose_f32_tile(Kind kind, int64_t M, int64_t N) {
     return &kF32Tiles[0];
 }
 
+int64_t tile_count(const GemmArgs& a, const Tile* t) { return ((a.M + t->bm - 1) / t->bm) * ((a.N + t->bn - 1) / t->bn); }
+
+// The register-staged tile a direct fp32 tile falls back to when it cannot
+// run a GEMM (same k order, so the same bits): the 256x128 and 128x256 twins,
+// and 256x128 for the 256x256 tile.
+const Tile* f32_register_twin(const Tile* t) {
+    if (!t->bk) return t;
+    return t == &kF32Tiles[5] ? &kF32Tiles[3] : &kF32Tiles[2];
+}
+
 // Direct-to-LDS twin of register tile t for GEMM `kind`, or null.  The
 // direct kernels take the plain forward, dX and dW (with or without the db
 // side output): no masked operand, no dZ side output, K a multiple of 16 and
@@ -127,9 +139,11 @@ const Tile* choose_f32_tile(Kind kind, int64_t M, int64_t N) {
 // fragment reads issued before the next tile's DMA), dW with db 128.5 ->
 // 134.6, without db 138.7.
 const Tile* f32_direct(Kind kind, const GemmArgs& a, const Tile* t, bool vec) {
-    if (t->bk) t = t->bm == 256 ? &kF32Tiles[2] : &kF32Tiles[3];  // forced twin: decide as for its register tile
     const bool plain = kind == Kind::Fwd || kind == Kind::Dx || kind == Kind::Dw;
     if (!plain || a.Amask || a.Bmask || a.dz || !vec || a.K < 16 || a.K % 16 != 0) return nullptr;
+    if (t == &kF32Tiles[6]) return kind == Kind::Fwd ? nullptr : t;  // forced 256x256 (dX, dW only)
+    if (t->bk) t = f32_register_twin(t);  // forced twin: decide as for its register tile
+    if (!f32_forced() && kind != Kind::Fwd && tile_count(a, &kF32Tiles[6]) >= 256) return &kF32Tiles[6];
     if (t == &kF32Tiles[2]) return &kF32Tiles[4];
     if (t == &kF32Tiles[3]) return &kF32Tiles[5];
     return nullptr;
@@ -168,7 +182,6 @@ bool direct_eligible(Kind kind, const GemmArgs& a, const Tile* t) {
     return a.K > 0 && a.M >= 8 && a.N >= 8 && k_ok(a, t);
 }
 
-int64_t tile_count(const GemmArgs& a, const Tile* t) { return ((a.M + t->bm - 1) / t->bm) * ((a.N + t->bn - 1) / t->bn); }
 
 // Split-K factor for direct tile t: the largest power of two S <= 32 with
 // tiles * S <= max_blocks, each split at least min_k deep and a multiple of
@@ -458,7 +471,7 @@ int run_gemm(int dtype, Kind kind, const GemmArgs& a0, bool a_kc, bool b_kc, hip
         void* args[] = {&a};
         return launch(name, dim3((unsigned)blocks), dim3(d->threads), args, stream);
     }
-    if (t->bk) t = t->bm == 256 ? &kF32Tiles[2] : &kF32Tiles[3];
+    t = f32_register_twin(t);
     if (const int S = plan_split_f32(a, t)) return run_split_f32(kind, a, t, S, vec, stream, ws);
     char name[96];
     std::snprintf(name, sizeof(name), "c3_gemm_f32_%s_%s_%s", kind_name(kind), t->name, vec ? "v" : "s");

@@ -55,6 +55,7 @@ def test_code_objects_hold_every_dispatched_kernel():
     for kind in ["fwd", "dx", "dw"]:
         for tile in ["t256x128d", "t128x256d"]:
             assert f"c3_gemm_f32_{kind}_{tile}" in gemm
+    assert {"c3_gemm_f32_dx_t256x256d", "c3_gemm_f32_dw_t256x256d"} <= gemm
     for name in ["c3_gemm_f32_bwd_t64x64", "c3_gemm_f32_bwd_mask_t64x64"]:
         assert f"{name}_v" in gemm and f"{name}_s" in gemm
     ew = _kernel_symbols(LIB / "elementwise.hsaco")
@@ -135,7 +136,8 @@ def test_backward_chain_validation():
 
 
 def test_gemm_tile_override_validation():
-    assert native.gemm_tile_names(native.F32) == ["t64x64", "t128x128", "t256x128", "t128x256", "t256x128d", "t128x256d"]
+    assert native.gemm_tile_names(native.F32) == ["t64x64", "t128x128", "t256x128", "t128x256", "t256x128d", "t128x256d",
+                                                  "t256x256d"]
     assert native.gemm_tile_names(native.BF16) == ["t64x64", "t128x128", "t256x128", "t256x256", "d256w8", "d256rq", "d256pp", "d128w4"]
     L = native.load()
     assert L.c3hip_set_gemm_tile(native.F32, b"d256w8") == native.ERR_INVALID  # a bf16-only tile
