@@ -241,6 +241,26 @@ def test_f32_direct_tiles_match_register_tiles(gpu, stream, monkeypatch, pair, M
         assert_close_gemm(gb, rb, bound, FP32_TOL, what="db")
 
 
+@pytest.mark.parametrize("tile", ["t256x128d", "t128x256d", "t256x256d"])
+@pytest.mark.parametrize("M,K,Nn", [(512, 16, 256), (256, 32, 512), (16, 512, 272), (32, 48, 16)])
+def test_f32_direct_tiles_short_k_bit_exact(gpu, stream, monkeypatch, tile, M, K, Nn):
+    # One, two and three k-tiles through the three-stage pipeline (the
+    # prologue's second tile and the last waits), and extents below one tile:
+    # the forward (k = K), dX (k = N) and dW (k = M) on integer inputs against
+    # the oracle.
+    monkeypatch.setenv("C3_HIP_GEMM_TILE", tile)
+    X, W, Y, dY = _bwd_inputs(97, M, K, Nn, True)
+    b = ints(98, Nn)
+    Yg = empty((M, Nn))
+    N.linear_fwd(N.F32, ptr(dev(X)), ptr(dev(W)), ptr(dev(b)), ptr(Yg), M, K, Nn, 1, stream)
+    same_bits(host(Yg), O.linear_fwd(X, W, b, 1))
+    gX, gW, gb = _run_bwd(stream, X, W, Y, dY, 1)
+    rX, rW, rb = O.linear_bwd(X, W, Y, dY, 1)
+    same_bits(gX, rX)
+    same_bits(gW, rW)
+    same_bits(gb, rb)
+
+
 @pytest.mark.parametrize("M,K,Nn", BWD_SHAPES)
 @pytest.mark.parametrize("act", [1, 0])
 def test_linear_bwd_integer_bit_exact(gpu, stream, M, K, Nn, act):
