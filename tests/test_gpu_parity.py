@@ -261,6 +261,28 @@ def test_f32_direct_tiles_short_k_bit_exact(gpu, stream, monkeypatch, tile, M, K
     same_bits(gb, rb)
 
 
+@pytest.mark.parametrize("tile", [None, "t256x128d", "t256x256d"])
+def test_f32_direct_backward_specials(gpu, stream, monkeypatch, tile):
+    # The direct route's pre-pass forms dZ = (Y > 0 ? 1 : 0) * dY as one IEEE
+    # multiply: -0 and NaN in Y mask to zero, +inf in Y passes dY, a zero mask
+    # times an infinite or NaN dY gives NaN, which then reaches its dX row, dW
+    # column and db entry.  Integer elsewhere, so every other element is exact.
+    if tile:
+        monkeypatch.setenv("C3_HIP_GEMM_TILE", tile)
+    M, K, Nn = 512, 128, 256
+    X, W, Y, dY = _bwd_inputs(99, M, K, Nn, True)
+    rng = np.random.default_rng(100)
+    for v in (-0.0, np.nan, np.inf, -np.inf):
+        Y[rng.integers(0, M, 6), rng.integers(0, Nn, 6)] = v
+    for v in (-0.0, np.inf, -np.inf, np.nan):
+        dY[rng.integers(0, M, 3), rng.integers(0, Nn, 3)] = v
+    gX, gW, gb = _run_bwd(stream, X, W, Y, dY, 1)
+    rX, rW, rb = O.linear_bwd(X, W, Y, dY, 1)
+    same_bits(gX, rX)
+    same_bits(gW, rW)
+    same_bits(gb, rb)
+
+
 @pytest.mark.parametrize("M,K,Nn", BWD_SHAPES)
 @pytest.mark.parametrize("act", [1, 0])
 def test_linear_bwd_integer_bit_exact(gpu, stream, M, K, Nn, act):
