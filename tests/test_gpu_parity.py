@@ -335,8 +335,10 @@ def test_linear_bwd_mask_signs_and_nan(gpu, stream):
 
 # ------------------------------------------------------------- matmul ----
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
-@pytest.mark.parametrize("M,K,Nn", [(96, 64, 80), (130, 67, 129), (512, 256, 512)])
+@pytest.mark.parametrize("M,K,Nn", [(96, 64, 80), (130, 67, 129), (512, 256, 512), (4096, 64, 2048)])
 def test_matmul_transposes(gpu, stream, ta, tb, M, K, Nn):
+    # (4096, 64, 2048): grids large enough for the size heuristic's direct
+    # fp32 tiles on A.B, A.B^T and A^T.B (A^T.B^T stays register-staged).
     A = ints(61, (K, M) if ta else (M, K))
     B = ints(62, (Nn, K) if tb else (K, Nn))
     C = empty((M, Nn))
