@@ -130,14 +130,15 @@ const Tile* f32_register_twin(const Tile* t) {
     return t == &kF32Tiles[5] ? &kF32Tiles[3] : &kF32Tiles[2];
 }
 
-// Direct-to-LDS twin of register tile t for GEMM `kind`, or null.  The
-// direct kernels take the plain forward, dX and dW (with or without the db
-// side output): no masked operand, no dZ side output, K a multiple of 16 and
-// vector-aligned operands (vec).  Measured on MI355X at 8192x4096x4096,
-// alternating with the register kernels in one process (bit-identical
-// outputs): forward 132.5 -> 139.0 TFLOP/s, dX 133 -> 138.5 (its first
-// fragment reads issued before the next tile's DMA), dW with db 128.5 ->
-// 134.6, without db 138.7.
+// Direct-to-LDS tile for GEMM `kind` whose register tile is t, or null: the
+// 256x256 tile for dX and dW on grids of at least 256 such tiles, else the
+// twin of t.  The direct kernels take the plain forward, dX and dW (with or
+// without the db side output): no masked operand, no dZ side output, K a
+// multiple of 16 and vector-aligned operands (vec).  Measured on MI355X at
+// 8192x4096x4096, alternating with the register kernels in one process
+// (bit-identical outputs): forward 132.5 -> 139.0 TFLOP/s, dX 133 -> 138.5
+// (its first fragment reads issued before the next tile's DMA; 141.0 on
+// 256x256), dW with db 128.5 -> 134.6, without db 138.7 (139.6 on 256x256).
 const Tile* f32_direct(Kind kind, const GemmArgs& a, const Tile* t, bool vec) {
     const bool plain = kind == Kind::Fwd || kind == Kind::Dx || kind == Kind::Dw;
     if (!plain || a.Amask || a.Bmask || a.dz || !vec || a.K < 16 || a.K % 16 != 0) return nullptr;
