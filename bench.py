@@ -368,11 +368,13 @@ def bench_bf16(torch, C, dev, s, args):
         step()
     ms, _, kt = _timed_steps(torch, C, torch.cuda.current_stream(), step, args.steps)
     tf = 6.0 * M * N * K / (ms * 1e-3) / 1e12
-    # The three GEMMs (forward, dX, dW) each do 2 M N K flop per launch; the
-    # backward pre-pass (dZ and the db partials) and the db reduction are HBM streams.
+    # The forward GEMM does 2 M N K flop per launch, the backward's dX and dW
+    # 4 M N K together, in one launch (c3_gemm_bf16_bwd_*) or two; the
+    # backward pre-pass (dZ and the db partials) is an HBM stream.
     gemms = {k: v for k, v in kt.items() if k.startswith("c3_gemm_")}
     dom = max(gemms, key=lambda k: gemms[k]["avg_ms"])
-    ach = 2.0 * M * N * K / (gemms[dom]["avg_ms"] * 1e-3) / 1e12
+    dom_flop = (4.0 if dom.startswith("c3_gemm_bf16_bwd_") else 2.0) * M * N * K
+    ach = dom_flop / (gemms[dom]["avg_ms"] * 1e-3) / 1e12
     return {"workload": "same layer, bf16 storage, fp32 accumulate", "ms_per_step": round(ms, 4),
             "tflops": round(tf, 2), "frac_of_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4), "kernels": kt,
             "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(ach, 2), "peak": PEAK_BF16_TFLOPS,

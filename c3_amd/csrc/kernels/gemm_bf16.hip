@@ -323,10 +323,15 @@ struct DirectTile {
     static constexpr int RC_CPR = ROWS / 8;           // RC: 16-byte chunks per k-row
     static_assert(BYTES % (1024 * NWAVES) == 0, "tile must split into whole instructions per wave");
     static_assert(BK == 32 || BK == 64, "BK is 32 or 64");
-    static_assert(KC || ROWS >= 64, "RC swizzle needs >= 8 chunks per k-row");
+    static_assert(KC || ROWS == 64 || ROWS >= 128, "RC swizzle keys are for 8 or >= 16 chunks per k-row");
     uint32_t goff[NI];
 
     __device__ __forceinline__ static int kc_key(int r) { return BK == 64 ? ((r >> 1) & 7) : ((r >> 2) & 3); }
+    // RC: k-rows of >= 256 bytes start on bank 0 (key 4 (kr % 4) over 16
+    // chunks); 128-byte k-rows (ROWS = 64) put two k-rows on each 256-byte
+    // bank row, so k-rows kr and kr + 1 already differ by 8 bank groups and
+    // the key 4 ((kr / 2) % 2) over 8 chunks separates kr from kr + 2.
+    __device__ __forceinline__ static int rc_key(int kr) { return ROWS >= 128 ? 4 * (kr & 3) : 4 * ((kr >> 1) & 1); }
 
     // grow0: first global row (m or n) of the tile; rows_total bounds it.
     __device__ __forceinline__ void init(int wave, int lane, int64_t ld, int64_t grow0, int64_t rows_total) {
@@ -341,7 +346,7 @@ struct DirectTile {
                 goff[i] = (uint32_t)(gr * ld + 8 * c);
             } else {
                 const int kr = q * (64 / RC_CPR) + lane / RC_CPR;
-                const int c = (lane % RC_CPR) ^ (4 * (kr & 3));
+                const int c = (lane % RC_CPR) ^ rc_key(kr);
                 int64_t gc = grow0 + 8 * c;
                 if (gc > rows_total - 8) gc = rows_total - 8;
                 goff[i] = (uint32_t)(kr * ld + gc);
@@ -384,9 +389,9 @@ struct DirectTile {
     // operands, any for RC ones): lanes whose 16-byte chunk lies below kr
     // issue their DMA as issue() does; the others write zeros to the LDS slot
     // their DMA would fill, so the fragments past kr are exact zeros and
-    // nothing beyond the operand is read.  Used only by 2-stage kernels, whose
-    // tile waits are vmcnt(0), so a wave that skips its DMA instructions does
-    // not upset the wait counts.
+    // nothing beyond the operand is read.  A wave may skip DMA instructions
+    // here, so every tile wait from the issue of this tile on is vmcnt(0)
+    // (the kernels' counted waits assume NI instructions per tile).
     __device__ __forceinline__ void issue_partial(const unsigned short* P, unsigned short* S, int wave, int lane,
                                                   int kr) const {
 #pragma unroll
@@ -435,7 +440,7 @@ struct DirectTile {
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 const int kr = 16 * st + 8 * (G >> 1) + 4 * h + (sp >> 2);
-                const int slot = (col >> 3) ^ (4 * (kr & 3));
+                const int slot = (col >> 3) ^ rc_key(kr);
                 v[h] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(S + kr * ROWS + slot * 8 + (col & 7)));
             }
             i16x8 w = {v[0][0], v[0][1], v[0][2], v[0][3], v[1][0], v[1][1], v[1][2], v[1][3]};
@@ -451,13 +456,22 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-// Wait until at most `after` tiles' DMA instructions (NIW per tile) are outstanding.
+// Wait until at most min(after, J) tiles' DMA instructions (NIW per tile)
+// are outstanding.
+template <int NIW, int J>
+__device__ __forceinline__ void wait_tiles_upto(int after) {
+    if constexpr (J == 0) {
+        wait_vmcnt<0>();
+    } else {
+        if (after >= J) wait_vmcnt<J * NIW>();
+        else wait_tiles_upto<NIW, J - 1>(after);
+    }
+}
+
+// Wait until at most `after` (< PF) tiles' DMA instructions are outstanding.
 template <int NIW, int PF>
 __device__ __forceinline__ void wait_tiles_after(int after) {
-    if (PF >= 4 && after >= 3) wait_vmcnt<(PF >= 4 ? 3 : 0) * NIW>();
-    else if (PF >= 3 && after >= 2) wait_vmcnt<(PF >= 3 ? 2 : 0) * NIW>();
-    else if (after >= 1) wait_vmcnt<NIW>();
-    else wait_vmcnt<0>();
+    wait_tiles_upto<NIW, PF - 1>(after);
 }
 
 // Epilogue of the direct kernels.  Their MFMAs take the B fragment as the
@@ -587,8 +601,17 @@ __device__ __forceinline__ void store_tile_t(const GemmArgs& p, f32x16 (&acc)[FM
 // 8192x4096x4096 forward +7% (1026 -> 1096 TF/s), dX +1%, dW +0.3%; at
 // 16384x8192x8192 +2% / +3% / +0.5%.  Issuing the last k-step's MFMAs after
 // the next tile's barrier as well (so they cover that barrier) was 1-3% slower.
+// The LDS stages of a direct kernel: one array per size, so the two GEMM
+// bodies of a layer-backward launch (same tile) share it.
+template <int ELEMS>
+__device__ __forceinline__ unsigned short* direct_smem() {
+    __shared__ __attribute__((aligned(1024))) unsigned short smem[ELEMS];
+    return smem;
+}
+
+// bid: the block's index among this GEMM's blocks (blockIdx.x by default).
 template <int WAVES_M, int WAVES_N, bool AK, bool BKC, int EPI, int BK, int STAGES, int BM, int BN, bool EARLY = false>
-__device__ __forceinline__ void gemm_bf16_direct_body(const GemmArgs& p) {
+__device__ __forceinline__ void gemm_bf16_direct_body(const GemmArgs& p, int bid = -1) {
     constexpr int NW = WAVES_M * WAVES_N;
     constexpr int TM = BM / WAVES_M, TN = BN / WAVES_N, FM = TM / 32, FN = TN / 32;
     constexpr int PF = STAGES - 1;  // tiles in flight ahead of the one multiplied
@@ -598,7 +621,7 @@ __device__ __forceinline__ void gemm_bf16_direct_body(const GemmArgs& p) {
     constexpr int NIW = TA::NI + TB::NI;
     static_assert(PF * NIW < 64, "outstanding DMA instructions exceed vmcnt");
 
-    __shared__ __attribute__((aligned(1024))) unsigned short smem[STAGES * STAGE];
+    unsigned short* const smem = direct_smem<STAGES * STAGE>();
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -606,7 +629,7 @@ __device__ __forceinline__ void gemm_bf16_direct_body(const GemmArgs& p) {
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
 
     int tm, tn;
-    tile_coords<8>(p.M, p.N, BM, BN, tm, tn);
+    tile_coords<8>(p.M, p.N, BM, BN, tm, tn, bid);
     const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
 
     const unsigned short* A = (const unsigned short*)p.A;
@@ -626,15 +649,17 @@ __device__ __forceinline__ void gemm_bf16_direct_body(const GemmArgs& p) {
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-    // k-tiles; the last one holds kr_last valid k (BK when K % BK == 0; only
-    // 2-stage kernels are launched with K % BK != 0).
+    // k-tiles; the last one holds kr_last valid k (BK when K % BK == 0).  A
+    // partial last tile skips the DMA instructions of its invalid chunks, so
+    // once it is issued (from iteration nk - PF on) the waits are vmcnt(0).
     const int nk = (int)((p.K + BK - 1) / BK);
     const int kr_last = (int)(p.K - (int64_t)(nk - 1) * BK);
+    const int k_exact_until = kr_last < BK ? nk - PF : nk;
     const uint32_t smem_lds = __builtin_amdgcn_readfirstlane(
         (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)smem);
     auto issue_tile = [&](int t, int stage) {
         unsigned short* S = smem + stage * STAGE;
-        if (STAGES == 2 && t == nk - 1 && kr_last < BK) {
+        if (t == nk - 1 && kr_last < BK) {
             la.issue_partial(A + (int64_t)t * a_kstep, S, wave, lane, kr_last);
             lb.issue_partial(B + (int64_t)t * b_kstep, S + A_EL, wave, lane, kr_last);
         } else if (EARLY) {
@@ -652,7 +677,7 @@ __device__ __forceinline__ void gemm_bf16_direct_body(const GemmArgs& p) {
     }
 
     for (int kt = 0; kt < nk; ++kt) {
-        wait_tiles_after<NIW, PF>(min(nk - 1 - kt, PF - 1));
+        wait_tiles_after<NIW, PF>(kt < k_exact_until ? min(nk - 1 - kt, PF - 1) : 0);
         __syncthreads();
         const unsigned short* As = smem + (kt % STAGES) * STAGE;
         const unsigned short* Bs = As + A_EL;
@@ -972,6 +997,45 @@ C3_GEMM_BF16_D_KINDS(d256w8, 2, 4, 64, 2, 256)
 // two blocks per CU): four times the blocks of d256w8 for grids too small to
 // fill the chip with 256x256 tiles.
 C3_GEMM_BF16_D_KINDS(d128w4, 2, 2, 64, 2, 128)
+// d128w4s4: the same tiles with 4 stages (128 KiB, one block per CU, three
+// tiles in flight) for grids of one block per CU over long k.
+C3_GEMM_BF16_D_KINDS(d128w4s4, 2, 2, 64, 4, 128)
+// d64w4: 64x64 tiles, 4 waves of 32x32, 64-deep k, 4 stages (64 KiB): grids
+// of 1024x1024 outputs, where 128x128 tiles leave three quarters of the CUs
+// idle and a 2-stage pipeline exposes the memory latency at every k-tile.
+C3_GEMM_BF16_D_KINDS(d64w4, 2, 2, 64, 4, 64)
+
+// The layer backward after its pre-pass in one launch: blocks [0, nx)
+// compute dX = dZ . W^T (the dx kind), [nx, nx + nw) dW = X^T . dZ (the dw
+// kind), and [nx + nw, nx + nw + nf) the bias gradient's final pass over the
+// pre-pass's chunk partials (64 columns per block, c3_colsum_final_f32's
+// order).  A block runs one of the three bodies, so the results are those of
+// the separate launches; the launch boundaries between them go.
+struct Bf16BwdArgs {
+    GemmArgs dx;
+    GemmArgs dw;
+    const float* part;  // [nchunks, dw.N] column partials (nf > 0)
+    float* db;
+    int64_t nchunks;
+    int nx, nw;
+};
+
+#define C3_GEMM_BF16_BWD(T, WM, WN, BK, ST, BT)                                                              \
+    extern "C" __global__ __launch_bounds__(64 * WM * WN) void c3_gemm_bf16_bwd_##T(Bf16BwdArgs p) {        \
+        __shared__ float red[8][64];                                                                          \
+        const int b = blockIdx.x;                                                                             \
+        if (b < p.nx)                                                                                         \
+            gemm_bf16_direct_body<WM, WN, true, true, 0, BK, ST, BT, BT, true>(p.dx, b);                     \
+        else if (b < p.nx + p.nw)                                                                             \
+            gemm_bf16_direct_body<WM, WN, false, false, 2, BK, ST, BT, BT, true>(p.dw, b - p.nx);            \
+        else                                                                                                  \
+            colsum_final_block<WM * WN>(p.part, p.db, p.nchunks, p.dw.N, b - p.nx - p.nw, red);              \
+    }
+
+C3_GEMM_BF16_BWD(d256w8, 2, 4, 64, 2, 256)
+C3_GEMM_BF16_BWD(d128w4, 2, 2, 64, 2, 128)
+C3_GEMM_BF16_BWD(d128w4s4, 2, 2, 64, 4, 128)
+C3_GEMM_BF16_BWD(d64w4, 2, 2, 64, 4, 64)
 
 
 

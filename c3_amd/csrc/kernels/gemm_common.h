@@ -131,3 +131,40 @@ __device__ __forceinline__ u32x4 mask_mul8(u32x4 y, u32x4 d) {
     return u32x4{mask_mul2(y[0], d[0]), mask_mul2(y[1], d[1]), mask_mul2(y[2], d[2]), mask_mul2(y[3], d[3])};
 }
 
+// ---- column-sum final pass ----
+// out[j] = sum over chunks c of part[c * N + j] for the 64 columns
+// j = 64 b .. 64 b + 63: virtual wave w (of 8) adds chunks w, w + 8, ...
+// into four interleaved sums (chunks c, c + 8, c + 16, c + 24 per step of
+// 32), and the eight wave sums are added in wave order.  A block of NW waves
+// runs 8 / NW virtual waves per wave, so every NW gives the same bits.
+// red: 8 x 64 floats of LDS.
+template <int NW>
+__device__ __forceinline__ void colsum_final_block(const float* __restrict__ part, float* __restrict__ out,
+                                                   int64_t nchunks, int64_t N, int64_t b, float (*red)[64]) {
+    static_assert(NW == 1 || NW == 2 || NW == 4 || NW == 8, "8 virtual waves over NW waves");
+    const int lane = threadIdx.x & 63, w0 = threadIdx.x >> 6;
+    const int64_t j = b * 64 + lane;
+#pragma unroll
+    for (int v = 0; v < 8 / NW; ++v) {
+        const int w = w0 + NW * v;
+        float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+        if (j < N) {
+            int64_t c = w;
+            for (; c + 24 < nchunks; c += 32) {
+                s0 += part[c * N + j];
+                s1 += part[(c + 8) * N + j];
+                s2 += part[(c + 16) * N + j];
+                s3 += part[(c + 24) * N + j];
+            }
+            for (; c < nchunks; c += 8) s0 += part[c * N + j];
+        }
+        red[w][lane] = (s0 + s1) + (s2 + s3);
+    }
+    __syncthreads();
+    if (w0 == 0 && j < N) {
+        float t = red[0][lane];
+#pragma unroll
+        for (int k = 1; k < 8; ++k) t += red[k][lane];
+        out[j] = t;
+    }
+}

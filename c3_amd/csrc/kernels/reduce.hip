@@ -21,6 +21,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "gemm_common.h"
+
 constexpr int kThreads = 256;
 
 // mask (nullable, same layout as in): sums (mask > 0 ? 1 : 0) * in, the bias
@@ -54,31 +56,12 @@ extern "C" __global__ __launch_bounds__(kThreads) void c3_colsum_partial_f32(
 
 // Pass 2: out[j] = sum over chunks of part[c][j].  Block: 64 columns x 8
 // waves; wave w adds chunks w, w + 8, ... into four interleaved sums, and the
-// eight wave sums are added in wave order.  Grid: ceil(N / 64).
+// eight wave sums are added in wave order (colsum_final_block, which the bf16
+// layer-backward launch also runs).  Grid: ceil(N / 64).
 extern "C" __global__ __launch_bounds__(512) void c3_colsum_final_f32(
     const float* __restrict__ part, float* __restrict__ out, int64_t nchunks, int64_t N) {
     __shared__ float red[8][64];
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int64_t j = (int64_t)blockIdx.x * 64 + lane;
-    float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
-    if (j < N) {
-        int64_t c = w;
-        for (; c + 24 < nchunks; c += 32) {
-            s0 += part[c * N + j];
-            s1 += part[(c + 8) * N + j];
-            s2 += part[(c + 16) * N + j];
-            s3 += part[(c + 24) * N + j];
-        }
-        for (; c < nchunks; c += 8) s0 += part[c * N + j];
-    }
-    red[w][lane] = (s0 + s1) + (s2 + s3);
-    __syncthreads();
-    if (w == 0 && j < N) {
-        float t = red[0][lane];
-#pragma unroll
-        for (int k = 1; k < 8; ++k) t += red[k][lane];
-        out[j] = t;
-    }
+    colsum_final_block<8>(part, out, nchunks, N, blockIdx.x, red);
 }
 
 // One wave per row.
@@ -102,7 +85,6 @@ extern "C" __global__ __launch_bounds__(kThreads) void c3_rowsum_f32(
 // column sums of dZ in fp32 into part [nchunks, N] when non-null (the bias
 // gradient, finished by c3_colsum_final_f32).  Each step is one IEEE
 // operation in the order written (no multiply-add contraction).
-#include "gemm_common.h"
 
 __device__ __forceinline__ float act_grad(float y, float d, int act) {
 #pragma clang fp contract(off)

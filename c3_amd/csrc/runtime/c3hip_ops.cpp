@@ -171,7 +171,9 @@ const Tile* choose_bf16_tile(int64_t M, int64_t N) {
 const Tile kBf16Direct[] = {{"d256w8", 256, 256, 512, 64, true},
                              {"d256rq", 256, 256, 256, 64, false},
                              {"d256pp", 256, 256, 512, 32, false},
-                             {"d128w4", 128, 128, 256, 64, true}};
+                             {"d128w4", 128, 128, 256, 64, true},
+                             {"d128w4s4", 128, 128, 256, 64, true},
+                             {"d64w4", 64, 64, 256, 64, true}};
 
 // K a multiple of the tile's k depth, or any K for a tile with a partial
 // last k-tile (whose k-contiguous operands have K % 8 == 0 by the 16-byte
@@ -202,10 +204,11 @@ int plan_split(const GemmArgs& a, const Tile* t, int64_t max_blocks, int64_t min
 // Split plan of a forced direct tile: as the size heuristic would split it
 // (fewer tiles than one block per CU), else 1.
 int forced_split(const GemmArgs& a, const Tile* t) {
-    const bool small = t->bm == 128;
-    const int64_t per_wave = small ? 512 : 256;  // blocks resident at once (two 128x128 blocks per CU)
+    // Blocks resident at once: two per CU for the 64 KiB tiles, else one.
+    const bool two = std::strcmp(t->name, "d128w4") == 0 || std::strcmp(t->name, "d64w4") == 0;
+    const int64_t per_wave = two ? 512 : 256;
     if (tile_count(a, t) >= per_wave / 2) return 1;
-    return plan_split(a, t, per_wave, small ? 256 : 512);
+    return plan_split(a, t, per_wave, t->bm == 128 ? 256 : 512);
 }
 
 // Sets *unsupported when the calling thread forced a direct tile this
@@ -214,12 +217,15 @@ int forced_split(const GemmArgs& a, const Tile* t) {
 //  - 256x256 tiles when they give at least 256 blocks (one per CU), or, for
 //    a weight gradient, reach 256 blocks with k split into parts at least
 //    4096 deep;
+//  - else 64x64 tiles (4 stages) when 128x128 tiles give fewer than 128
+//    blocks, 64x64 tiles at least 256, and K <= 8192;
 //  - else 128x128 tiles when they give at least 128 blocks, or for K >= 2048
 //    when split-K brings them there; below 256 blocks the k range is split
-//    into parts at least 512 deep, up to 512 blocks (two per CU);
+//    into parts at least 512 deep, up to 512 blocks (two per CU); 128 to 256
+//    blocks over K >= 2048 without a split take the 4-stage variant;
 //  - else, for a weight gradient, 128x128 tiles when splits at least 256
 //    deep reach 256 blocks;
-//  - else the register-staged kernels (best for a 1024^3-sized forward and dX).
+//  - else the register-staged kernels (outputs smaller than 1024x1024).
 const Tile* choose_bf16_direct(Kind kind, const GemmArgs& a, bool* unsupported, int* split) {
     *unsupported = false;
     *split = 1;
@@ -259,8 +265,21 @@ const Tile* choose_bf16_direct(Kind kind, const GemmArgs& a, bool* unsupported, 
         }
     }
     const int64_t tiles_s = tile_count(a, small);
+    // Outputs too small for 128 128x128 tiles whose 64x64 tiles fill the chip
+    // (a 1024x1024 output): 64x64 tiles, no split, up to k = 8192.  Measured
+    // on MI355X at 1024x1024x1024 (forward / dX / dW): 8.3 / 7.4 / 7.5 us
+    // against 18.2 / 10.8 / 18.7 for the register-staged 64x64 tile and the
+    // split 128x128 dW; k = 4096: 19.5-20.3 us against 26.7-28.4 for split
+    // 128x128 tiles; k = 8192 36.2 against 37.3.
+    const Tile* tiny = find_tile(kBf16Direct, nd, "d64w4");
+    if (tiles_s < 128 && tile_count(a, tiny) >= 256 && a.K <= 8192) return tiny;
     const int Ss = tiles_s >= 256 ? 1 : plan_split(a, small, 512, 512);  // 256 blocks: one per CU already
     if (tiles_s >= 128 || (a.K >= 2048 && tiles_s * Ss >= 128)) {
+        // One block per CU over k >= 2048 (no split): four stages, three
+        // tiles in flight.  Measured on MI355X on the 256-tile GEMMs of the
+        // 4096 / 1024 sweep shapes with k = 4096: 44.0-46.5 us against
+        // 46.6-50.1 for two stages; equal at k = 1024.
+        if (Ss == 1 && tiles_s <= 256 && a.K >= 2048) return find_tile(kBf16Direct, nd, "d128w4s4");
         *split = Ss;
         return small;
     }
@@ -578,13 +597,48 @@ int colsum(const float* in, const float* mask, float* out, int64_t M, int64_t N,
     return release_workspace(part, how, rc, stream, "column-sum partials");
 }
 
+// Arguments of c3_gemm_bf16_bwd_<tile> (gemm_bf16.hip).
+struct Bf16BwdArgs {
+    GemmArgs dx;
+    GemmArgs dw;
+    const float* part;
+    float* db;
+    int64_t nchunks;
+    int nx, nw;
+};
+
+// The direct tile on which the size heuristic runs both GEMMs of a bf16
+// layer backward (ax: dX, aw: dW) without a split, when no tile is forced;
+// else null.  Those run as one launch (c3_gemm_bf16_bwd_<tile>) together
+// with the bias gradient's final pass.  Measured on MI355X against the
+// separate launches, alternating in one process over the 27 sweep shapes
+// (bit-identical outputs): 1024^3 backward 24.5 -> 19.5 us, 1024x4096x1024
+// 44.2 -> 33.4, 4096^3 270 -> 262; the others within 1%.
+const Tile* bf16_bwd_pair_tile(const GemmArgs& ax, const GemmArgs& aw) {
+    if (bf16_forced()) return nullptr;
+    if (!bf16_vec_ok(true, ax.M, ax.K, ax.lda, ax.A, nullptr) || !bf16_vec_ok(true, ax.N, ax.K, ax.ldb, ax.B, nullptr) ||
+        !bf16_vec_ok(false, aw.M, aw.K, aw.lda, aw.A, nullptr) || !bf16_vec_ok(false, aw.N, aw.K, aw.ldb, aw.B, nullptr))
+        return nullptr;
+    bool unsupported = false;
+    int sx = 1, sw = 1;
+    const Tile* tx = choose_bf16_direct(Kind::Dx, ax, &unsupported, &sx);
+    const Tile* tw = choose_bf16_direct(Kind::Dw, aw, &unsupported, &sw);
+    if (!tx || tx != tw || sx != 1 || sw != 1) return nullptr;
+    if (std::strcmp(tx->name, "d256w8") && std::strcmp(tx->name, "d128w4") && std::strcmp(tx->name, "d128w4s4") &&
+        std::strcmp(tx->name, "d64w4"))
+        return nullptr;
+    if (tile_count(ax, tx) + tile_count(aw, tw) + (aw.N + 63) / 64 > 0x7fffffff) return nullptr;
+    return tx;
+}
+
 // Backward through a pre-pass: one pass forms dZ = act'(Y) * dY (in the
 // layer's dtype, a workspace of the call) together with the per-chunk column
 // sums for db, then dX and dW run as plain GEMMs on dZ.  Used for every bf16
 // backward (the direct-to-LDS kernels cannot apply a mask while loading), for
 // the fp32 sigmoid/tanh backward (the fp32 GEMMs fuse only the ReLU mask), and
 // for the fp32 ReLU backward whose plain dX and dW run direct (f32_bwd_direct).
-// Without an activation, dZ is dY itself.
+// Without an activation, dZ is dY itself.  bf16 dX, dW and the db final
+// pass go in one launch where bf16_bwd_pair_tile allows.
 int linear_bwd_prepass(int dtype, const void* X, const void* W, const void* Y, const void* dY, void* dX, float* dW,
                        float* db, int64_t M, int64_t K, int64_t N, int act, hipStream_t stream) {
     const size_t esz = dtype == C3HIP_BF16 ? 2 : 4;
@@ -622,28 +676,41 @@ int linear_bwd_prepass(int dtype, const void* X, const void* W, const void* Y, c
         if (dz) (void)release_workspace(dz, dz_how, rc, stream, "dZ");
         return rc;
     }
+    const void* dzp = need_dz ? dz : dY;
+    GemmArgs ax{};
+    ax.A = dzp; ax.B = W; ax.C = dX;
+    ax.M = M; ax.N = K; ax.K = N;
+    ax.lda = N; ax.ldb = N; ax.ldc = K;
+    GemmArgs aw{};
+    aw.A = X; aw.B = dzp; aw.C = dW;
+    aw.M = K; aw.N = N; aw.K = M;
+    aw.lda = K; aw.ldb = N; aw.ldc = N;
+    const Tile* pair = dtype == C3HIP_BF16 && dX && dW && K > 0 ? bf16_bwd_pair_tile(ax, aw) : nullptr;
     if (need_dz || db) {
         float* part_out = db ? (nchunks > 1 ? part : db) : nullptr;
         int act_i = act;
         void* args[] = {(void*)&Y, (void*)&dY, &dz, &part_out, &M, &N, &rows_per_chunk, &act_i, &vb};
         rc = launch(dtype == C3HIP_BF16 ? "c3_dz_colsum_bf16" : f32v ? "c3_dz_colsum_f32_v" : "c3_dz_colsum_f32",
                     dim3(g.gx, (unsigned)nchunks), dim3(256), args, stream);
-        if (rc == C3HIP_OK && db && nchunks > 1) rc = colsum_final(part, db, nchunks, N, stream);
+        if (rc == C3HIP_OK && db && nchunks > 1 && !pair) rc = colsum_final(part, db, nchunks, N, stream);
     }
-    const void* dzp = need_dz ? dz : dY;
-    if (rc == C3HIP_OK && dX) {
-        GemmArgs a{};
-        a.A = dzp; a.B = W; a.C = dX;
-        a.M = M; a.N = K; a.K = N;
-        a.lda = N; a.ldb = N; a.ldc = K;
-        rc = run_gemm(dtype, Kind::Dx, a, true, true, stream);
-    }
-    if (rc == C3HIP_OK && dW) {
-        GemmArgs a{};
-        a.A = X; a.B = dzp; a.C = dW;
-        a.M = K; a.N = N; a.K = M;
-        a.lda = K; a.ldb = N; a.ldc = N;
-        rc = run_gemm(dtype, Kind::Dw, a, false, false, stream);
+    if (rc == C3HIP_OK && pair) {
+        Bf16BwdArgs p{};
+        p.dx = ax;
+        p.dw = aw;
+        p.nx = (int)tile_count(ax, pair);
+        p.nw = (int)tile_count(aw, pair);
+        const int64_t nf = db && nchunks > 1 ? (N + 63) / 64 : 0;
+        p.part = part;
+        p.db = db;
+        p.nchunks = nchunks;
+        char name[64];
+        std::snprintf(name, sizeof(name), "c3_gemm_bf16_bwd_%s", pair->name);
+        void* args[] = {&p};
+        rc = launch(name, dim3((unsigned)(p.nx + p.nw + nf)), dim3(pair->threads), args, stream);
+    } else {
+        if (rc == C3HIP_OK && dX) rc = run_gemm(dtype, Kind::Dx, ax, true, true, stream);
+        if (rc == C3HIP_OK && dW) rc = run_gemm(dtype, Kind::Dw, aw, false, false, stream);
     }
     if (part) rc = release_workspace(part, part_how, rc, stream, "column-sum partials");
     if (dz) rc = release_workspace(dz, dz_how, rc, stream, "dZ");

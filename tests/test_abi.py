@@ -58,6 +58,13 @@ def test_code_objects_hold_every_dispatched_kernel():
     assert {"c3_gemm_f32_dx_t256x256d", "c3_gemm_f32_dw_t256x256d"} <= gemm
     for name in ["c3_gemm_f32_bwd_t64x64", "c3_gemm_f32_bwd_mask_t64x64"]:
         assert f"{name}_v" in gemm and f"{name}_s" in gemm
+    bf = _kernel_symbols(LIB / "gemm_bf16.hsaco")
+    for tile in ["d256w8", "d256rq", "d256pp", "d128w4", "d128w4s4", "d64w4"]:
+        for kind in ["fwd", "dx", "dw", "dwb", "tt", "fwdt", "fwdf", "dxf", "ttf"]:
+            assert f"c3_gemm_bf16_{kind}_{tile}" in bf
+    for tile in ["d256w8", "d128w4", "d128w4s4", "d64w4"]:  # layer backward in one launch
+        assert f"c3_gemm_bf16_bwd_{tile}" in bf
+    assert {"c3_splitk_reduce", "c3_transpose_bf16"} <= bf
     ew = _kernel_symbols(LIB / "elementwise.hsaco")
     for op in list(native.EW_OPS) + list(native.EW_MATH_OPS):
         assert f"c3_ew_{op}_f32_v" in ew and f"c3_ew_{op}_f32_s" in ew
@@ -138,7 +145,7 @@ def test_backward_chain_validation():
 def test_gemm_tile_override_validation():
     assert native.gemm_tile_names(native.F32) == ["t64x64", "t128x128", "t256x128", "t128x256", "t256x128d", "t128x256d",
                                                   "t256x256d"]
-    assert native.gemm_tile_names(native.BF16) == ["t64x64", "t128x128", "t256x128", "t256x256", "d256w8", "d256rq", "d256pp", "d128w4"]
+    assert native.gemm_tile_names(native.BF16) == ["t64x64", "t128x128", "t256x128", "t256x256", "d256w8", "d256rq", "d256pp", "d128w4", "d128w4s4", "d64w4"]
     L = native.load()
     assert L.c3hip_set_gemm_tile(native.F32, b"d256w8") == native.ERR_INVALID  # a bf16-only tile
     assert L.c3hip_set_gemm_tile(native.BF16, b"t32x32") == native.ERR_INVALID

@@ -401,7 +401,8 @@ def test_bf16_integer_bit_exact(gpu, stream, M, K, Nn, act):
     same_bits(host(db), rb)
 
 
-@pytest.mark.parametrize("tile", ["d256w8", "d256rq", "d256pp", "d128w4", "t64x64", "t128x128", "t256x128", "t256x256"])
+@pytest.mark.parametrize("tile", ["d256w8", "d256rq", "d256pp", "d128w4", "d128w4s4", "d64w4", "t64x64", "t128x128",
+                                  "t256x128", "t256x256"])
 def test_every_bf16_tile_bit_exact(gpu, stream, monkeypatch, tile):
     # Each bf16 kernel family forced for the forward and every backward GEMM,
     # on ragged M and N (the 256x256 tiles run 2x2 blocks with partial edges).
@@ -424,7 +425,7 @@ def test_every_bf16_tile_bit_exact(gpu, stream, monkeypatch, tile):
     same_bits(host(db), rb)
 
 
-@pytest.mark.parametrize("tile", [None, "d256w8", "d128w4"])
+@pytest.mark.parametrize("tile", [None, "d256w8", "d128w4", "d128w4s4", "d64w4"])
 @pytest.mark.parametrize("M,K,Nn", [(328, 1000, 264), (301, 1000, 264), (200, 72, 136), (264, 40, 8)])
 def test_bf16_direct_k_tail_bit_exact(gpu, stream, monkeypatch, tile, M, K, Nn):
     # k extents that are not multiples of the direct kernels' 64-deep k-tile:
@@ -523,7 +524,7 @@ def test_forced_tile_override(gpu, stream):
             args = (N.BF16, ptr(dev_bf16(X)), ptr(dev_bf16(W)), ptr(dev(b)), ptr(Y), M, K, Nn, 1, stream)
             # K = 264 is not a multiple of the direct tiles' 32/64-deep k tile: those
             # with a partial last k-tile run it, the others refuse it.
-            if tile.startswith("d") and tile not in ("d256w8", "d128w4"):
+            if tile.startswith("d") and tile not in ("d256w8", "d128w4", "d128w4s4", "d64w4"):
                 with pytest.raises(N.C3HipError) as e:
                     N.linear_fwd(*args)
                 assert e.value.code == N.ERR_UNSUPPORTED
@@ -566,7 +567,7 @@ def test_bf16_pingpong_short_k_bit_exact(gpu, stream, monkeypatch, K):
 # shape splits one GEMM of the layer: (576, 8192, 576) the forward,
 # (576, 576, 8192) dX (k = N), (8192, 576, 576) dW (k = M); 576 = 9 x 64, so
 # every forced direct tile runs all three GEMMs.
-@pytest.mark.parametrize("tile", [None, "d256w8", "d256rq", "d256pp", "d128w4"])
+@pytest.mark.parametrize("tile", [None, "d256w8", "d256rq", "d256pp", "d128w4", "d128w4s4", "d64w4"])
 @pytest.mark.parametrize("M,K,Nn", [(576, 8192, 576), (576, 576, 8192), (8192, 576, 576)])
 def test_bf16_split_k_bit_exact(gpu, stream, monkeypatch, tile, M, K, Nn):
     from tests.parity import dev_bf16
@@ -593,6 +594,47 @@ def test_bf16_split_k_bit_exact(gpu, stream, monkeypatch, tile, M, K, Nn):
     same_bits(host(dX), _bf16_round((dZ @ W64.T).astype(np.float32)))
     same_bits(host(dW), (X64.T @ dZ).astype(np.float32))
     same_bits(host(db), dZ.sum(axis=0).astype(np.float32))
+
+
+# The bf16 layer backward after its pre-pass runs dX, dW and the bias
+# gradient's final pass in one launch (c3_gemm_bf16_bwd_<tile>) where the size
+# heuristic puts both GEMMs on one direct tile without a split.  Forcing that
+# same tile (no split on these shapes either) turns the one-launch path off:
+# the separate dX, dW and column-sum launches must give the same bits on
+# real-valued inputs.  One shape per tile the one-launch path covers.
+@pytest.mark.parametrize("M,K,Nn,tile", [(1000, 1016, 1024, "d64w4"), (1024, 4096, 1024, "d128w4"),
+                                         (2048, 2048, 2048, "d128w4s4"), (4096, 4096, 4096, "d256w8")])
+def test_bf16_layer_backward_one_launch_matches_separate(gpu, stream, M, K, Nn, tile):
+    from tests.parity import dev_bf16
+
+    rng = np.random.default_rng(M + K + Nn)
+    X = dev_bf16(rng.standard_normal((M, K), dtype=np.float32))
+    W = dev_bf16(rng.standard_normal((K, Nn), dtype=np.float32) / np.float32(np.sqrt(K)))
+    Y = dev_bf16(rng.standard_normal((M, Nn), dtype=np.float32))
+    dY = dev_bf16(rng.standard_normal((M, Nn), dtype=np.float32))
+
+    def bwd():
+        dX = empty((M, K), dtype=torch.bfloat16)
+        dW, db = empty((K, Nn)), empty(Nn)
+        N.set_launch_timing(True)
+        try:
+            N.linear_bwd(N.BF16, ptr(X), ptr(W), ptr(Y), ptr(dY), ptr(dX), ptr(dW), ptr(db), M, K, Nn, 1, stream)
+            names = [n for n, _ in N.launch_timings()]
+        finally:
+            N.set_launch_timing(False)
+        return [host(dX), host(dW), host(db)], names
+
+    one, names = bwd()
+    assert names == ["c3_dz_colsum_bf16", f"c3_gemm_bf16_bwd_{tile}"], names
+    N.set_gemm_tile(N.BF16, tile)
+    try:
+        sep, names = bwd()
+    finally:
+        N.set_gemm_tile(N.BF16, None)
+    assert names == ["c3_dz_colsum_bf16", "c3_colsum_final_f32", f"c3_gemm_bf16_dx_{tile}",
+                     f"c3_gemm_bf16_dw_{tile}"], names
+    for got, ref in zip(one, sep):
+        same_bits(got, ref)
 
 
 def test_bf16_split_k_real_values(gpu, stream):
