@@ -1020,22 +1020,29 @@ struct Bf16BwdArgs {
     int nx, nw;
 };
 
-#define C3_GEMM_BF16_BWD(T, WM, WN, BK, ST, BT)                                                              \
-    extern "C" __global__ __launch_bounds__(64 * WM * WN) void c3_gemm_bf16_bwd_##T(Bf16BwdArgs p) {        \
+// dX on one direct tile (X-suffixed parameters), dW on another with the
+// same block size and LDS stages of the same size (one array, shared).
+#define C3_GEMM_BF16_BWD2(NAME, WMX, WNX, STX, BTX, WMW, WNW, STW, BTW)                                     \
+    extern "C" __global__ __launch_bounds__(64 * WMX * WNX) void NAME(Bf16BwdArgs p) {                     \
+        static_assert(WMX * WNX == WMW * WNW, "one block size");                                             \
         __shared__ float red[8][64];                                                                          \
         const int b = blockIdx.x;                                                                             \
         if (b < p.nx)                                                                                         \
-            gemm_bf16_direct_body<WM, WN, true, true, 0, BK, ST, BT, BT, true>(p.dx, b);                     \
+            gemm_bf16_direct_body<WMX, WNX, true, true, 0, 64, STX, BTX, BTX, true>(p.dx, b);                \
         else if (b < p.nx + p.nw)                                                                             \
-            gemm_bf16_direct_body<WM, WN, false, false, 2, BK, ST, BT, BT, true>(p.dw, b - p.nx);            \
+            gemm_bf16_direct_body<WMW, WNW, false, false, 2, 64, STW, BTW, BTW, true>(p.dw, b - p.nx);       \
         else                                                                                                  \
-            colsum_final_block<WM * WN>(p.part, p.db, p.nchunks, p.dw.N, b - p.nx - p.nw, red);              \
+            colsum_final_block<WMX * WNX>(p.part, p.db, p.nchunks, p.dw.N, b - p.nx - p.nw, red);            \
     }
+#define C3_GEMM_BF16_BWD(T, WM, WN, ST, BT) C3_GEMM_BF16_BWD2(c3_gemm_bf16_bwd_##T, WM, WN, ST, BT, WM, WN, ST, BT)
 
-C3_GEMM_BF16_BWD(d256w8, 2, 4, 64, 2, 256)
-C3_GEMM_BF16_BWD(d128w4, 2, 2, 64, 2, 128)
-C3_GEMM_BF16_BWD(d128w4s4, 2, 2, 64, 4, 128)
-C3_GEMM_BF16_BWD(d64w4, 2, 2, 64, 4, 64)
+C3_GEMM_BF16_BWD(d256w8, 2, 4, 2, 256)
+C3_GEMM_BF16_BWD(d128w4, 2, 2, 2, 128)
+C3_GEMM_BF16_BWD(d128w4s4, 2, 2, 4, 128)
+C3_GEMM_BF16_BWD(d64w4, 2, 2, 4, 64)
+// 64x64 and 128x128 tiles: 4 waves and 64 KiB of LDS stages each.
+C3_GEMM_BF16_BWD2(c3_gemm_bf16_bwd_d64w4_d128w4, 2, 2, 4, 64, 2, 2, 2, 128)
+C3_GEMM_BF16_BWD2(c3_gemm_bf16_bwd_d128w4_d64w4, 2, 2, 2, 128, 2, 2, 4, 64)
 
 
 

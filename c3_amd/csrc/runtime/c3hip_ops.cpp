@@ -607,28 +607,30 @@ struct Bf16BwdArgs {
     int nx, nw;
 };
 
-// The direct tile on which the size heuristic runs both GEMMs of a bf16
-// layer backward (ax: dX, aw: dW) without a split, when no tile is forced;
-// else null.  Those run as one launch (c3_gemm_bf16_bwd_<tile>) together
-// with the bias gradient's final pass.  Measured on MI355X against the
-// separate launches, alternating in one process over the 27 sweep shapes
-// (bit-identical outputs): 1024^3 backward 24.5 -> 19.5 us, 1024x4096x1024
-// 44.2 -> 33.4, 4096^3 270 -> 262; the others within 1%.
-const Tile* bf16_bwd_pair_tile(const GemmArgs& ax, const GemmArgs& aw) {
-    if (bf16_forced()) return nullptr;
+// Whether the size heuristic runs both GEMMs of a bf16 layer backward (ax:
+// dX, aw: dW) on direct tiles without a split and a one-launch kernel
+// (c3_gemm_bf16_bwd_<dX tile>[_<dW tile>]) exists for the two tiles: the
+// same tile, or the 64x64 and 128x128 tiles (same block size and LDS); no
+// tile forced.  That launch also runs the bias gradient's final pass.
+// Measured on MI355X against the separate launches, alternating in one
+// process over the 27 sweep shapes (bit-identical outputs): 1024^3
+// backward 24.5 -> 19.5 us, 1024x4096x1024 44.2 -> 33.4, 4096^3 270 -> 262;
+// the others within 1%.
+bool bf16_bwd_pair_tiles(const GemmArgs& ax, const GemmArgs& aw, const Tile** tx, const Tile** tw) {
+    if (bf16_forced()) return false;
     if (!bf16_vec_ok(true, ax.M, ax.K, ax.lda, ax.A, nullptr) || !bf16_vec_ok(true, ax.N, ax.K, ax.ldb, ax.B, nullptr) ||
         !bf16_vec_ok(false, aw.M, aw.K, aw.lda, aw.A, nullptr) || !bf16_vec_ok(false, aw.N, aw.K, aw.ldb, aw.B, nullptr))
-        return nullptr;
+        return false;
     bool unsupported = false;
     int sx = 1, sw = 1;
-    const Tile* tx = choose_bf16_direct(Kind::Dx, ax, &unsupported, &sx);
-    const Tile* tw = choose_bf16_direct(Kind::Dw, aw, &unsupported, &sw);
-    if (!tx || tx != tw || sx != 1 || sw != 1) return nullptr;
-    if (std::strcmp(tx->name, "d256w8") && std::strcmp(tx->name, "d128w4") && std::strcmp(tx->name, "d128w4s4") &&
-        std::strcmp(tx->name, "d64w4"))
-        return nullptr;
-    if (tile_count(ax, tx) + tile_count(aw, tw) + (aw.N + 63) / 64 > 0x7fffffff) return nullptr;
-    return tx;
+    *tx = choose_bf16_direct(Kind::Dx, ax, &unsupported, &sx);
+    *tw = choose_bf16_direct(Kind::Dw, aw, &unsupported, &sw);
+    if (!*tx || !*tw || sx != 1 || sw != 1) return false;
+    auto is = [](const Tile* t, const char* n) { return std::strcmp(t->name, n) == 0; };
+    const bool same = *tx == *tw && (is(*tx, "d256w8") || is(*tx, "d128w4") || is(*tx, "d128w4s4") || is(*tx, "d64w4"));
+    const bool mixed = (is(*tx, "d64w4") && is(*tw, "d128w4")) || (is(*tx, "d128w4") && is(*tw, "d64w4"));
+    if (!same && !mixed) return false;
+    return tile_count(ax, *tx) + tile_count(aw, *tw) + (aw.N + 63) / 64 <= 0x7fffffff;
 }
 
 // Backward through a pre-pass: one pass forms dZ = act'(Y) * dY (in the
@@ -638,7 +640,7 @@ const Tile* bf16_bwd_pair_tile(const GemmArgs& ax, const GemmArgs& aw) {
 // the fp32 sigmoid/tanh backward (the fp32 GEMMs fuse only the ReLU mask), and
 // for the fp32 ReLU backward whose plain dX and dW run direct (f32_bwd_direct).
 // Without an activation, dZ is dY itself.  bf16 dX, dW and the db final
-// pass go in one launch where bf16_bwd_pair_tile allows.
+// pass go in one launch where bf16_bwd_pair_tiles allows.
 int linear_bwd_prepass(int dtype, const void* X, const void* W, const void* Y, const void* dY, void* dX, float* dW,
                        float* db, int64_t M, int64_t K, int64_t N, int act, hipStream_t stream) {
     const size_t esz = dtype == C3HIP_BF16 ? 2 : 4;
@@ -685,7 +687,8 @@ int linear_bwd_prepass(int dtype, const void* X, const void* W, const void* Y, c
     aw.A = X; aw.B = dzp; aw.C = dW;
     aw.M = K; aw.N = N; aw.K = M;
     aw.lda = K; aw.ldb = N; aw.ldc = N;
-    const Tile* pair = dtype == C3HIP_BF16 && dX && dW && K > 0 ? bf16_bwd_pair_tile(ax, aw) : nullptr;
+    const Tile *px = nullptr, *pw = nullptr;
+    const bool pair = dtype == C3HIP_BF16 && dX && dW && K > 0 && bf16_bwd_pair_tiles(ax, aw, &px, &pw);
     if (need_dz || db) {
         float* part_out = db ? (nchunks > 1 ? part : db) : nullptr;
         int act_i = act;
@@ -698,16 +701,17 @@ int linear_bwd_prepass(int dtype, const void* X, const void* W, const void* Y, c
         Bf16BwdArgs p{};
         p.dx = ax;
         p.dw = aw;
-        p.nx = (int)tile_count(ax, pair);
-        p.nw = (int)tile_count(aw, pair);
+        p.nx = (int)tile_count(ax, px);
+        p.nw = (int)tile_count(aw, pw);
         const int64_t nf = db && nchunks > 1 ? (N + 63) / 64 : 0;
         p.part = part;
         p.db = db;
         p.nchunks = nchunks;
         char name[64];
-        std::snprintf(name, sizeof(name), "c3_gemm_bf16_bwd_%s", pair->name);
+        if (px == pw) std::snprintf(name, sizeof(name), "c3_gemm_bf16_bwd_%s", px->name);
+        else std::snprintf(name, sizeof(name), "c3_gemm_bf16_bwd_%s_%s", px->name, pw->name);
         void* args[] = {&p};
-        rc = launch(name, dim3((unsigned)(p.nx + p.nw + nf)), dim3(pair->threads), args, stream);
+        rc = launch(name, dim3((unsigned)(p.nx + p.nw + nf)), dim3(px->threads), args, stream);
     } else {
         if (rc == C3HIP_OK && dX) rc = run_gemm(dtype, Kind::Dx, ax, true, true, stream);
         if (rc == C3HIP_OK && dW) rc = run_gemm(dtype, Kind::Dw, aw, false, false, stream);

@@ -597,14 +597,20 @@ def test_bf16_split_k_bit_exact(gpu, stream, monkeypatch, tile, M, K, Nn):
 
 
 # The bf16 layer backward after its pre-pass runs dX, dW and the bias
-# gradient's final pass in one launch (c3_gemm_bf16_bwd_<tile>) where the size
-# heuristic puts both GEMMs on one direct tile without a split.  Forcing that
-# same tile (no split on these shapes either) turns the one-launch path off:
-# the separate dX, dW and column-sum launches must give the same bits on
-# real-valued inputs.  One shape per tile the one-launch path covers.
-@pytest.mark.parametrize("M,K,Nn,tile", [(1000, 1016, 1024, "d64w4"), (1024, 4096, 1024, "d128w4"),
-                                         (2048, 2048, 2048, "d128w4s4"), (4096, 4096, 4096, "d256w8")])
-def test_bf16_layer_backward_one_launch_matches_separate(gpu, stream, M, K, Nn, tile):
+# gradient's final pass in one launch (c3_gemm_bf16_bwd_<dX tile>[_<dW tile>])
+# where the size heuristic puts both GEMMs on direct tiles without a split.
+# A forced tile turns the one-launch path off: the separate dX, dW and
+# column-sum launches on it (no split on these shapes either) must give the
+# same bits on real-valued inputs (every direct tile adds k in the same
+# order).  One shape per one-launch kernel, with each activation's pre-pass
+# on the smallest.
+@pytest.mark.parametrize("M,K,Nn,pair,tile,act", [
+    (1000, 1016, 1024, "d64w4", "d64w4", 1), (1000, 1016, 1024, "d64w4", "d64w4", 2),
+    (1000, 1016, 1024, "d64w4", "d64w4", 3), (1000, 1016, 1024, "d64w4", "d64w4", 0),
+    (1024, 4096, 1024, "d128w4", "d128w4", 1), (2048, 2048, 2048, "d128w4s4", "d128w4s4", 1),
+    (4096, 4096, 4096, "d256w8", "d256w8", 1), (1024, 1024, 4096, "d64w4_d128w4", "d64w4", 1),
+    (4096, 1024, 1024, "d128w4_d64w4", "d64w4", 1)])
+def test_bf16_layer_backward_one_launch_matches_separate(gpu, stream, M, K, Nn, pair, tile, act):
     from tests.parity import dev_bf16
 
     rng = np.random.default_rng(M + K + Nn)
@@ -618,14 +624,14 @@ def test_bf16_layer_backward_one_launch_matches_separate(gpu, stream, M, K, Nn, 
         dW, db = empty((K, Nn)), empty(Nn)
         N.set_launch_timing(True)
         try:
-            N.linear_bwd(N.BF16, ptr(X), ptr(W), ptr(Y), ptr(dY), ptr(dX), ptr(dW), ptr(db), M, K, Nn, 1, stream)
+            N.linear_bwd(N.BF16, ptr(X), ptr(W), ptr(Y), ptr(dY), ptr(dX), ptr(dW), ptr(db), M, K, Nn, act, stream)
             names = [n for n, _ in N.launch_timings()]
         finally:
             N.set_launch_timing(False)
         return [host(dX), host(dW), host(db)], names
 
     one, names = bwd()
-    assert names == ["c3_dz_colsum_bf16", f"c3_gemm_bf16_bwd_{tile}"], names
+    assert names == ["c3_dz_colsum_bf16", f"c3_gemm_bf16_bwd_{pair}"], names
     N.set_gemm_tile(N.BF16, tile)
     try:
         sep, names = bwd()
