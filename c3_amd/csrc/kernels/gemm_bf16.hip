@@ -280,8 +280,8 @@ C3_GEMM_BF16_KINDS(t256x256, 256, 256, 2, 2)
 
 // ===========================================================================
 // Direct-to-LDS kernels: 256x256 block tiles (8 waves of 128x64, 4 waves of
-// 128x128, or 8 ping-pong waves) or 128x128 tiles (4 waves of 64x64),
-// BK-deep k tiles in STAGES LDS stages.
+// 128x128, or 8 ping-pong waves), 128x128 tiles (4 waves of 64x64) or 64x64
+// tiles (4 waves of 32x32), BK-deep k tiles in STAGES LDS stages.
 // Global tiles go straight into LDS with global_load_lds_dwordx4 (lane l's
 // 16 bytes land at base + 16*l of the instruction's 1 KiB), so no staging
 // registers and no LDS stores are needed.  Layouts, per operand:
@@ -292,7 +292,8 @@ C3_GEMM_BF16_KINDS(t256x256, 256, 256, 2, 2)
 //     ds_read_b128 fragment read touches fall into distinct banks; keying on
 //     r & 7 leaves a 2-way conflict.  Fragment: one ds_read_b128.
 //   RC (row contiguous in global): LDS [BK k][ROWS], the chunk holding rows
-//     8c..8c+7 of k-row kr sits in slot c ^ (4 * (kr % 4)).  A k-row is
+//     8c..8c+7 of k-row kr sits in slot c ^ (4 * (kr % 4)) (64-row tiles:
+//     c ^ (4 * ((kr / 2) % 2)), see rc_key).  A k-row of a 256-row tile is
 //     512 bytes, so every k-row starts on bank 0; the 32 lanes of one half of
 //     a transposed read address k-rows kbase..kbase+3 and chunks c0..c0+3,
 //     and the key 4 * (kr % 4) puts those 16 (kr, c) pairs on 16 distinct
@@ -592,6 +593,14 @@ __device__ __forceinline__ void store_tile_t(const GemmArgs& p, f32x16 (&acc)[FM
         store_blocks_t<EPI, 0, FM, FN, 0>(p, acc, mb, nb, vec, lane);
 }
 
+// The LDS stages of a direct kernel: one array per size, so the two GEMM
+// bodies of a layer-backward launch (tiles with stages of one size) share it.
+template <int ELEMS>
+__device__ __forceinline__ unsigned short* direct_smem() {
+    __shared__ __attribute__((aligned(1024))) unsigned short smem[ELEMS];
+    return smem;
+}
+
 // EARLY: after each tile barrier, issue the first k-step's fragment reads
 // before the DMA of the next tile (whose inline asm orders memory), with the
 // LDS addresses of the stages computed once.  The DMA issue is ~50 scalar
@@ -601,14 +610,6 @@ __device__ __forceinline__ void store_tile_t(const GemmArgs& p, f32x16 (&acc)[FM
 // 8192x4096x4096 forward +7% (1026 -> 1096 TF/s), dX +1%, dW +0.3%; at
 // 16384x8192x8192 +2% / +3% / +0.5%.  Issuing the last k-step's MFMAs after
 // the next tile's barrier as well (so they cover that barrier) was 1-3% slower.
-// The LDS stages of a direct kernel: one array per size, so the two GEMM
-// bodies of a layer-backward launch (same tile) share it.
-template <int ELEMS>
-__device__ __forceinline__ unsigned short* direct_smem() {
-    __shared__ __attribute__((aligned(1024))) unsigned short smem[ELEMS];
-    return smem;
-}
-
 // bid: the block's index among this GEMM's blocks (blockIdx.x by default).
 template <int WAVES_M, int WAVES_N, bool AK, bool BKC, int EPI, int BK, int STAGES, int BM, int BN, bool EARLY = false>
 __device__ __forceinline__ void gemm_bf16_direct_body(const GemmArgs& p, int bid = -1) {
