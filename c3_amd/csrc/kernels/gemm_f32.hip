@@ -523,12 +523,24 @@ __device__ __forceinline__ void f32_wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, bool AK, bool BKC, bool DB, bool EARLY = false>
+// Wait until at most min(after, J) tiles' DMA instructions (NIW per tile)
+// are outstanding.
+template <int NIW, int J>
+__device__ __forceinline__ void f32_wait_tiles_upto(int after) {
+    if constexpr (J == 0) {
+        f32_wait_vmcnt<0>();
+    } else {
+        if (after >= J) f32_wait_vmcnt<J * NIW>();
+        else f32_wait_tiles_upto<NIW, J - 1>(after);
+    }
+}
+
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool AK, bool BKC, bool DB, bool EARLY = false, int STAGES = 3>
 __device__ __forceinline__ void gemm_f32_direct_body(const GemmArgs& p) {
     constexpr int NT = 64 * WAVES_M * WAVES_N, NW = WAVES_M * WAVES_N;
     constexpr int TM = BM / WAVES_M, TN = BN / WAVES_N;
     constexpr int FM = TM / 32, FN = TN / 32;
-    constexpr int STAGES = 3, PF = STAGES - 1;
+    constexpr int PF = STAGES - 1;
     using TA = F32DirectTile<BM, AK, NW>;
     using TB = F32DirectTile<BN, BKC, NW>;
     constexpr int STAGE = TA::FLOATS + TB::FLOATS;
@@ -586,8 +598,7 @@ __device__ __forceinline__ void gemm_f32_direct_body(const GemmArgs& p) {
         // it (min(nk - 1 - kt, PF - 1) of them) is outstanding; the barrier
         // then makes every wave's part visible and ends every read of the
         // stage refilled below (tile kt - 1's).
-        if (kt + 1 < nk) f32_wait_vmcnt<NIW>();
-        else f32_wait_vmcnt<0>();
+        f32_wait_tiles_upto<NIW, PF - 1>(min(nk - 1 - kt, PF - 1));
         __syncthreads();
         const float* As = smem + (kt % STAGES) * STAGE;
         const float* Bs = As + TA::FLOATS;
@@ -646,6 +657,12 @@ __device__ __forceinline__ void gemm_f32_direct_body(const GemmArgs& p) {
     extern "C" __global__ __launch_bounds__(64 * WM * WN, 1) void NAME(GemmArgs p) {       \
         gemm_f32_direct_body<BM, BN, WM, WN, AK, BKC, DB, E>(p);                            \
     }
+// With ST LDS stages and split-K (block row y takes its k range, as the
+// register kernels do).
+#define C3_GEMM_F32_DS(NAME, BM, BN, WM, WN, AK, BKC, DB, E, ST)                              \
+    extern "C" __global__ __launch_bounds__(64 * WM * WN) void NAME(GemmArgs p) {              \
+        gemm_f32_direct_body<BM, BN, WM, WN, AK, BKC, DB, E, ST>(split_args_f32<AK, BKC>(p));    \
+    }
 // fwd: X (KC) . W (RC); dx: dZ (KC) . W^T (KC); dw: X^T (RC) . dZ (RC), db
 // when p.db is set.  The dX kinds issue each tile's first fragment reads
 // before the next tile's DMA (EARLY); measured on MI355X at 8192x4096x4096
@@ -664,3 +681,9 @@ C3_GEMM_F32_D_KINDS(t128x256d, 128, 256, 2, 4)
 // forward is faster on 256x128, 139.2 against 137.9).
 C3_GEMM_F32_D(c3_gemm_f32_dx_t256x256d, 256, 256, 2, 4, true, true, false, true)
 C3_GEMM_F32_D(c3_gemm_f32_dw_t256x256d, 256, 256, 2, 4, false, false, true, false)
+// 64x64: 4 waves of 32x32 and 6 LDS stages (five tiles in flight, 50 KiB)
+// for the small grids of the 64x64 register tile, whose k loop is a chain
+// of dependent memory round trips.
+C3_GEMM_F32_DS(c3_gemm_f32_fwd_t64x64d, 64, 64, 2, 2, true, false, false, false, 6)
+C3_GEMM_F32_DS(c3_gemm_f32_dx_t64x64d, 64, 64, 2, 2, true, true, false, true, 6)
+C3_GEMM_F32_DS(c3_gemm_f32_dw_t64x64d, 64, 64, 2, 2, false, false, true, false, 6)

@@ -72,14 +72,15 @@ struct Tile {
 // (elementwise.hip kVecThreads): one float4 per thread.
 constexpr int64_t kEwVecThreads = 64;
 
-// The last three are direct-to-LDS tiles (gemm_f32.hip, names ending in d):
+// The last four are direct-to-LDS tiles (gemm_f32.hip, names ending in d):
 // the twins of the register-staged 256x128 and 128x256 tiles (same blocks and
-// bits) and a 256x256 tile for dX and dW, taken for unmasked GEMMs with
-// K % 16 == 0 (f32_direct).  Every fp32 tile multiplies each output's k range
+// bits), a 256x256 tile for dX and dW and a 64x64 tile with 6 LDS stages,
+// taken for unmasked GEMMs with K % 16 == 0 (f32_direct).  Every fp32 tile multiplies each output's k range
 // in the same order, so all of them give the same bits.
 const Tile kF32Tiles[] = {{"t64x64", 64, 64, 256},        {"t128x128", 128, 128, 256}, {"t256x128", 256, 128, 512},
                           {"t128x256", 128, 256, 512},    {"t256x128d", 256, 128, 512, 16},
-                          {"t128x256d", 128, 256, 512, 16}, {"t256x256d", 256, 256, 512, 16}};
+                          {"t128x256d", 128, 256, 512, 16}, {"t256x256d", 256, 256, 512, 16},
+                          {"t64x64d", 64, 64, 256, 16}};
 const Tile kBf16Tiles[] = {{"t64x64", 64, 64, 256},
                            {"t128x128", 128, 128, 256},
                            {"t256x128", 256, 128, 256},
@@ -127,12 +128,14 @@ int64_t tile_count(const GemmArgs& a, const Tile* t) { return ((a.M + t->bm - 1)
 // and 256x128 for the 256x256 tile.
 const Tile* f32_register_twin(const Tile* t) {
     if (!t->bk) return t;
+    if (t == &kF32Tiles[7]) return &kF32Tiles[0];
     return t == &kF32Tiles[5] ? &kF32Tiles[3] : &kF32Tiles[2];
 }
 
 // Direct-to-LDS tile for GEMM `kind` whose register tile is t, or null: the
-// 256x256 tile for dX and dW on grids of at least 256 such tiles, else the
-// twin of t.  The direct kernels take the plain forward, dX and dW (with or
+// 256x256 tile for dX and dW on grids of at least 256 such tiles, the 64x64
+// direct tile for a forward on the 64x64 register tile's small grids, else
+// the twin of t.  The direct kernels take the plain forward, dX and dW (with or
 // without the db side output): no masked operand, no dZ side output, K a
 // multiple of 16 and vector-aligned operands (vec).  Measured on MI355X at
 // 8192x4096x4096, alternating with the register kernels in one process
@@ -143,10 +146,18 @@ const Tile* f32_direct(Kind kind, const GemmArgs& a, const Tile* t, bool vec) {
     const bool plain = kind == Kind::Fwd || kind == Kind::Dx || kind == Kind::Dw;
     if (!plain || a.Amask || a.Bmask || a.dz || !vec || a.K < 16 || a.K % 16 != 0) return nullptr;
     if (t == &kF32Tiles[6]) return kind == Kind::Fwd ? nullptr : t;  // forced 256x256 (dX, dW only)
+    if (t == &kF32Tiles[7]) return t;                                 // forced 64x64
     if (t->bk) t = f32_register_twin(t);  // forced twin: decide as for its register tile
     if (!f32_forced() && kind != Kind::Fwd && tile_count(a, &kF32Tiles[6]) >= 256) return &kF32Tiles[6];
     if (t == &kF32Tiles[2]) return &kF32Tiles[4];
     if (t == &kF32Tiles[3]) return &kF32Tiles[5];
+    // A forward on at most 256 64x64 tiles (at most one round of blocks):
+    // the 6-stage direct tile.  Measured on MI355X against the register
+    // 64x64 tile, alternating in one process (bit-identical outputs):
+    // 128x256x128 11.2 -> 9.8 us, 128x784x256 (split k) 12.8 -> 12.0,
+    // 1024^3 35.1 -> 28.5, 512x4096x512 118.9 -> 92.4; on 1024 tiles
+    // (2048x1024x2048) 85.1 -> 99.8, so larger grids keep the register tile.
+    if (t == &kF32Tiles[0] && kind == Kind::Fwd && !f32_forced() && tile_count(a, t) <= 256) return &kF32Tiles[7];
     return nullptr;
 }
 
@@ -423,7 +434,8 @@ int run_split_f32(Kind kind, const GemmArgs& a0, const Tile* t, int S, bool vec,
     g.split_k = split_k;
     g.c_split = slice;
     char name[96];
-    std::snprintf(name, sizeof(name), "c3_gemm_f32_%s_%s_%s", kind_name(kind), t->name, vec ? "v" : "s");
+    if (t->bk) std::snprintf(name, sizeof(name), "c3_gemm_f32_%s_%s", kind_name(kind), t->name);
+    else std::snprintf(name, sizeof(name), "c3_gemm_f32_%s_%s_%s", kind_name(kind), t->name, vec ? "v" : "s");
     void* args[] = {&g};
     rc = launch(name, dim3((unsigned)tile_count(a0, t), (unsigned)S), dim3(t->threads), args, stream);
     if (rc == C3HIP_OK) {
@@ -484,6 +496,8 @@ int run_gemm(int dtype, Kind kind, const GemmArgs& a0, bool a_kc, bool b_kc, hip
     // direct tile's register twin).
     const bool forced_reg = f32_forced() && !t->bk;
     if (const Tile* d = forced_reg ? nullptr : f32_direct(kind, a, t, vec)) {
+        if (d == &kF32Tiles[7])
+            if (const int S = plan_split_f32(a, &kF32Tiles[0])) return run_split_f32(kind, a, d, S, vec, stream, ws);
         char name[96];
         std::snprintf(name, sizeof(name), "c3_gemm_f32_%s_%s", kind_name(kind), d->name);
         const int64_t blocks = tile_count(a, d);

@@ -169,11 +169,11 @@ int c3hip_elementwise3(int op, int dtype, const void* a, const void* b, const vo
  * fallback); with a forced tile the bf16 layer backward runs dX, dW and the
  * bias gradient's final pass as separate launches (the size heuristic may
  * put them in one; the bits are the same).  The fp32 direct-to-LDS tiles
- * (t256x128d, t128x256d, t256x256d) run the plain forward (t256x256d: dX
- * and dW only), dX and dW with K a multiple of 16 on 16-byte aligned
- * operands; any other GEMM forced onto them runs on their register-staged
- * twin (t256x128, t128x256; t256x128 for t256x256d), which multiplies in the
- * same order, so the result is the same.  Replaces the optimisation-level choice of the reference's PGO
+ * (t256x128d, t128x256d, t256x256d, t64x64d) run the plain forward
+ * (t256x256d: dX and dW only), dX and dW with K a multiple of 16 on 16-byte
+ * aligned operands; any other GEMM forced onto them runs on their
+ * register-staged twin (t256x128, t128x256, t64x64; t256x128 for t256x256d),
+ * which multiplies in the same order, so the result is the same.  Replaces the optimisation-level choice of the reference's PGO
  * tiers (PGOCompiledKernel::compileO2 / compileOfast,
  * src/C3/PGOManager.cpp:292-366): here a tier differs by launch configuration,
  * which the tuner picks by timing the candidates on the caller's stream.

@@ -962,7 +962,7 @@ TEST(merged_kernel_runs_layers_in_order) {
 }
 
 // A PGO kernel: eager first (the interpreter) and the compile chain; then
-// the Ofast tuner times the seven fp32 tiles on real calls (the host kernels
+// the Ofast tuner times the eight fp32 tiles on real calls (the host kernels
 // sleep per tile, t128x128 fastest) and keeps the fastest; results are the
 // same on every tier.
 TEST(pgo_tiers_tune_and_deopt) {
@@ -978,6 +978,7 @@ TEST(pgo_tiers_tune_and_deopt) {
                        : sp.tile == "t256x128d" ? 7
                        : sp.tile == "t128x256d" ? 5
                        : sp.tile == "t256x256d" ? 3
+                       : sp.tile == "t64x64d"   ? 2
                                                 : 0;
         return std::make_shared<ScriptedKernel>(o.opt_level, [inner, ms](const std::vector<Tensor>& in) {
             if (ms) std::this_thread::sleep_for(std::chrono::milliseconds(ms));
@@ -997,14 +998,14 @@ TEST(pgo_tiers_tune_and_deopt) {
     CHECK_EQ(rig.interpreted.load(), 1);
     CHECK(k->isPromoted() && k->o2Kernel() && k->ofastKernel());
     auto tuners = k->tuners();
-    CHECK(tuners.size() == 1 && tuners[0] && tuners[0]->candidateCount() == 7);
+    CHECK(tuners.size() == 1 && tuners[0] && tuners[0]->candidateCount() == 8);
     int calls = 1;
     while (!tuners[0]->tuned() && calls < 40) {
         CHECK(vals(k->execute(in)[0]) == want);
         ++calls;
     }
     CHECK(tuners[0]->tuned());
-    CHECK_EQ(calls, 1 + 7 * (1 + P.config().tune_samples));
+    CHECK_EQ(calls, 1 + 8 * (1 + P.config().tune_samples));
     CHECK_EQ(tuners[0]->chosen(), std::string("t128x128"));
     CHECK(vals(k->execute(in)[0]) == want);
     CHECK_EQ(rig.interpreted.load(), 1);

@@ -53,7 +53,7 @@ def test_code_objects_hold_every_dispatched_kernel():
             for v in "vs":
                 assert f"c3_gemm_f32_{kind}_{tile}_{v}" in gemm
     for kind in ["fwd", "dx", "dw"]:
-        for tile in ["t256x128d", "t128x256d"]:
+        for tile in ["t256x128d", "t128x256d", "t64x64d"]:
             assert f"c3_gemm_f32_{kind}_{tile}" in gemm
     assert {"c3_gemm_f32_dx_t256x256d", "c3_gemm_f32_dw_t256x256d"} <= gemm
     for name in ["c3_gemm_f32_bwd_t64x64", "c3_gemm_f32_bwd_mask_t64x64"]:
@@ -144,7 +144,7 @@ def test_backward_chain_validation():
 
 def test_gemm_tile_override_validation():
     assert native.gemm_tile_names(native.F32) == ["t64x64", "t128x128", "t256x128", "t128x256", "t256x128d", "t128x256d",
-                                                  "t256x256d"]
+                                                  "t256x256d", "t64x64d"]
     assert native.gemm_tile_names(native.BF16) == ["t64x64", "t128x128", "t256x128", "t256x256", "d256w8", "d256rq", "d256pp", "d128w4", "d128w4s4", "d64w4"]
     L = native.load()
     assert L.c3hip_set_gemm_tile(native.F32, b"d256w8") == native.ERR_INVALID  # a bf16-only tile

@@ -170,7 +170,8 @@ def test_small_bwd_one_launch_matches_two(gpu, stream, monkeypatch, M, K, Nn, ac
     assert_close_gemm(one[1], rW, gemm_bound(X.T, O.relu_mask_mul(Y, dY) if act else dY, M), FP32_TOL, what="dW")
 
 
-@pytest.mark.parametrize("tile", ["t64x64", "t128x128", "t256x128", "t128x256", "t256x128d", "t128x256d", "t256x256d"])
+@pytest.mark.parametrize("tile", ["t64x64", "t128x128", "t256x128", "t128x256", "t256x128d", "t128x256d", "t256x256d",
+                                  "t64x64d"])
 @pytest.mark.parametrize("M,K,Nn", [(300, 260, 200), (257, 128, 64), (272, 144, 80)])
 def test_every_fp32_tile_bit_exact(gpu, stream, monkeypatch, tile, M, K, Nn):
     # Each tile the planner can pick, forced for every GEMM of the layer
@@ -189,7 +190,7 @@ def test_every_fp32_tile_bit_exact(gpu, stream, monkeypatch, tile, M, K, Nn):
 
 
 @pytest.mark.parametrize("tile", [None, "t64x64", "t128x128", "t256x128", "t128x256", "t256x128d", "t128x256d",
-                                  "t256x256d"])
+                                  "t256x256d", "t64x64d"])
 @pytest.mark.parametrize("M,K,Nn", [(1024, 768, 1536), (300, 260, 200), (2048, 1024, 4096)])
 def test_bwd_dz_side_output_matches_masked_launches(gpu, stream, monkeypatch, tile, M, K, Nn):
     # With dX and dW both asked for, the dX kernel also writes dZ = mask(Y) dY
@@ -211,7 +212,8 @@ def test_bwd_dz_side_output_matches_masked_launches(gpu, stream, monkeypatch, ti
     same_bits(both[2], gb)
 
 
-@pytest.mark.parametrize("pair", [("t256x128d", "t256x128"), ("t128x256d", "t128x256"), ("t256x256d", "t256x128")])
+@pytest.mark.parametrize("pair", [("t256x128d", "t256x128"), ("t128x256d", "t128x256"), ("t256x256d", "t256x128"),
+                                  ("t64x64d", "t64x64")])
 @pytest.mark.parametrize("M,K,Nn", [(512, 256, 384), (1000, 512, 776), (272, 144, 80), (300, 272, 200)])
 def test_f32_direct_tiles_match_register_tiles(gpu, stream, monkeypatch, pair, M, K, Nn):
     # The direct-to-LDS tiles (operands DMA'd into LDS, three stages) multiply
@@ -241,8 +243,8 @@ def test_f32_direct_tiles_match_register_tiles(gpu, stream, monkeypatch, pair, M
         assert_close_gemm(gb, rb, bound, FP32_TOL, what="db")
 
 
-@pytest.mark.parametrize("tile", ["t256x128d", "t128x256d", "t256x256d"])
-@pytest.mark.parametrize("M,K,Nn", [(512, 16, 256), (256, 32, 512), (16, 512, 272), (32, 48, 16)])
+@pytest.mark.parametrize("tile", ["t256x128d", "t128x256d", "t256x256d", "t64x64d"])
+@pytest.mark.parametrize("M,K,Nn", [(512, 16, 256), (256, 32, 512), (16, 512, 272), (32, 48, 16), (64, 96, 80)])
 def test_f32_direct_tiles_short_k_bit_exact(gpu, stream, monkeypatch, tile, M, K, Nn):
     # One, two and three k-tiles through the three-stage pipeline (the
     # prologue's second tile and the last waits), and extents below one tile:
