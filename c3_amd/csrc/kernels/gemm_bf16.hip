@@ -593,6 +593,59 @@ __device__ __forceinline__ void store_tile_t(const GemmArgs& p, f32x16 (&acc)[FM
         store_blocks_t<EPI, 0, FM, FN, 0>(p, acc, mb, nb, vec, lane);
 }
 
+// bf16 output of a wave's TM x TN tile through LDS (region: TM * TN bf16 of
+// the kernel's stages, free once every wave is past its last k-step): each
+// lane writes its 4-column groups (the values store_block_t computes, the
+// same operations) into a row-major copy whose 16-byte chunks are XOR-keyed
+// by row (r & 7), then reads back whole 16-byte chunks so that one store
+// instruction writes 8 rows x 128 contiguous bytes instead of 32 rows x 32.
+// Only for whole tiles with vector-aligned C (else store_tile_t).
+template <int EPI, int ACT, int FM, int FN>
+__device__ __forceinline__ void stage_tile_t(const GemmArgs& p, f32x16 (&acc)[FM][FN], int64_t mrow0, int64_t nb,
+                                             int lane, unsigned short* region) {
+    constexpr int TN = 32 * FN, RB = TN * 2;  // row bytes
+    const int h = lane >> 5;
+#pragma unroll
+    for (int q = 0; q < FN; ++q) {
+        const int64_t nq = nb + 32 * q;
+        float bv[16];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int64_t n = nq + 8 * (v >> 2) + 4 * h + (v & 3);
+            bv[v] = (EPI == 1 && p.bias != nullptr) ? p.bias[n] : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            const int r = 32 * i + (lane & 31);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                float x[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    x[e] = acc[i][q][4 * t + e];
+                    if (EPI == 1) {
+                        if (p.bias != nullptr) x[e] = x[e] + bv[4 * t + e];
+                        x[e] = act_c<ACT>(x[e]);
+                    }
+                }
+                const uint32_t w0 = (uint32_t)f32_to_bf16_rne(x[0]) | ((uint32_t)f32_to_bf16_rne(x[1]) << 16);
+                const uint32_t w1 = (uint32_t)f32_to_bf16_rne(x[2]) | ((uint32_t)f32_to_bf16_rne(x[3]) << 16);
+                const int chunk = 4 * q + t;
+                char* dst = (char*)region + r * RB + ((chunk ^ (r & 7)) * 16) + h * 8;
+                *(uint2*)dst = make_uint2(w0, w1);
+            }
+        }
+    }
+    constexpr int CPR = TN / 8, RPI = 64 / CPR;  // chunks per row, rows per instruction
+    const int cr = lane / CPR, ck = lane % CPR;
+#pragma unroll
+    for (int s = 0; s < 32 * FM / RPI; ++s) {
+        const int r = RPI * s + cr;
+        const u32x4 v = *(const u32x4*)((const char*)region + r * RB + ((ck ^ (r & 7)) * 16));
+        *(u32x4*)((unsigned short*)p.C + (mrow0 + r) * p.ldc + nb + 8 * ck) = v;
+    }
+}
+
 // The LDS stages of a direct kernel: one array per size, so the two GEMM
 // bodies of a layer-backward launch (tiles with stages of one size) share it.
 template <int ELEMS>
@@ -611,7 +664,8 @@ __device__ __forceinline__ unsigned short* direct_smem() {
 // 16384x8192x8192 +2% / +3% / +0.5%.  Issuing the last k-step's MFMAs after
 // the next tile's barrier as well (so they cover that barrier) was 1-3% slower.
 // bid: the block's index among this GEMM's blocks (blockIdx.x by default).
-template <int WAVES_M, int WAVES_N, bool AK, bool BKC, int EPI, int BK, int STAGES, int BM, int BN, bool EARLY = false>
+template <int WAVES_M, int WAVES_N, bool AK, bool BKC, int EPI, int BK, int STAGES, int BM, int BN, bool EARLY = false,
+          bool STAGED = false>
 __device__ __forceinline__ void gemm_bf16_direct_body(const GemmArgs& p, int bid = -1) {
     constexpr int NW = WAVES_M * WAVES_N;
     constexpr int TM = BM / WAVES_M, TN = BN / WAVES_N, FM = TM / 32, FN = TN / 32;
@@ -705,6 +759,20 @@ __device__ __forceinline__ void gemm_bf16_direct_body(const GemmArgs& p, int bid
         }
     }
 
+    if constexpr (STAGED && EPI != 2 && TN >= 64) {
+        static_assert(NW * TM * TN <= STAGES * STAGE, "staging fits the stages");
+        const int64_t mr = m0 + wm * TM, nc = n0 + wn * TN;
+        const bool whole = mr + TM <= p.M && nc + TN <= p.N && ((uintptr_t)p.C & 15) == 0 && (p.ldc & 7) == 0;
+        if (whole) {
+            __syncthreads();  // every wave past its last fragment read
+            unsigned short* region = smem + wave * (TM * TN);
+            if (EPI == 1)
+                with_act(p.act, [&](auto at) { stage_tile_t<EPI, decltype(at)::value, FM, FN>(p, acc, mr, nc, lane, region); });
+            else
+                stage_tile_t<EPI, 0, FM, FN>(p, acc, mr, nc, lane, region);
+            return;
+        }
+    }
     store_tile_t<EPI, FM, FN>(p, acc, m0 + wm * TM, n0 + wn * TN, lane);
 }
 
@@ -973,27 +1041,35 @@ __device__ __forceinline__ GemmArgs split_args(const GemmArgs& p) {
 C3_GEMM_BF16_PP_KINDS(d256pp, 32, 4)
 
 #define C3_GEMM_BF16_D(NAME, WM, WN, AK, BKC, EPI, BK, ST, BT) C3_GEMM_BF16_DE(NAME, WM, WN, AK, BKC, EPI, BK, ST, BT, false)
-#define C3_GEMM_BF16_DE(NAME, WM, WN, AK, BKC, EPI, BK, ST, BT, E)                                 \
-    extern "C" __global__ __launch_bounds__(64 * WM * WN) void NAME(GemmArgs p) {                 \
-        gemm_bf16_direct_body<WM, WN, AK, BKC, EPI, BK, ST, BT, BT, E>(split_args<AK, BKC, EPI>(p)); \
+#define C3_GEMM_BF16_DE(NAME, WM, WN, AK, BKC, EPI, BK, ST, BT, E) C3_GEMM_BF16_DES(NAME, WM, WN, AK, BKC, EPI, BK, ST, BT, E, false)
+#define C3_GEMM_BF16_DES(NAME, WM, WN, AK, BKC, EPI, BK, ST, BT, E, SG)                                    \
+    extern "C" __global__ __launch_bounds__(64 * WM * WN) void NAME(GemmArgs p) {                         \
+        gemm_bf16_direct_body<WM, WN, AK, BKC, EPI, BK, ST, BT, BT, E, SG>(split_args<AK, BKC, EPI>(p));   \
     }
 
 // fwd: X (KC) . W (RC) + bias, act -> bf16.  fwdt: the same with W given
 // transposed ([N, K], KC).  dx: dZ (KC) . W^T (KC) -> bf16.
 // dw: X^T (RC) . dZ (RC) -> fp32.  dwb: same, bf16 out.  tt: A^T (RC) . B^T (KC) -> bf16.
-#define C3_GEMM_BF16_D_KINDS(T, WM, WN, BK, ST, BT)                                        \
-    C3_GEMM_BF16_DE(c3_gemm_bf16_fwd_##T, WM, WN, true, false, 1, BK, ST, BT, true)         \
+// FSG: the bf16-output forwards store through LDS (stage_tile_t).
+#define C3_GEMM_BF16_D_KINDS(T, WM, WN, BK, ST, BT) C3_GEMM_BF16_D_KINDS_S(T, WM, WN, BK, ST, BT, false)
+#define C3_GEMM_BF16_D_KINDS_S(T, WM, WN, BK, ST, BT, FSG)                                 \
+    C3_GEMM_BF16_DES(c3_gemm_bf16_fwd_##T, WM, WN, true, false, 1, BK, ST, BT, true, FSG)   \
     C3_GEMM_BF16_DE(c3_gemm_bf16_dx_##T, WM, WN, true, true, 0, BK, ST, BT, true)           \
     C3_GEMM_BF16_DE(c3_gemm_bf16_dw_##T, WM, WN, false, false, 2, BK, ST, BT, true)         \
     C3_GEMM_BF16_DE(c3_gemm_bf16_dwb_##T, WM, WN, false, false, 0, BK, ST, BT, true)        \
     C3_GEMM_BF16_DE(c3_gemm_bf16_tt_##T, WM, WN, false, true, 0, BK, ST, BT, true)          \
-    C3_GEMM_BF16_DE(c3_gemm_bf16_fwdt_##T, WM, WN, true, true, 1, BK, ST, BT, true)         \
+    C3_GEMM_BF16_DES(c3_gemm_bf16_fwdt_##T, WM, WN, true, true, 1, BK, ST, BT, true, FSG)   \
     C3_GEMM_BF16_DE(c3_gemm_bf16_fwdf_##T, WM, WN, true, false, 2, BK, ST, BT, true)        \
     C3_GEMM_BF16_DE(c3_gemm_bf16_dxf_##T, WM, WN, true, true, 2, BK, ST, BT, true)          \
     C3_GEMM_BF16_DE(c3_gemm_bf16_ttf_##T, WM, WN, false, true, 2, BK, ST, BT, true)
 
 // d256w8: 256x256 tiles, 8 waves of 128x64, 64-deep k, 2 stages (128 KiB LDS).
-C3_GEMM_BF16_D_KINDS(d256w8, 2, 4, 64, 2, 256)
+// Its forwards store whole tiles through LDS: timed alternately in one
+// process against the direct stores (bit-identical outputs), forward
+// 8192x4096x4096 249.8 -> 241.4 us, 4096x1024x4096 40.2 -> 38.2, 16384x8192x8192
+// 1904 -> 1887; dX gained nothing (245.5 / 245.4, 240.4 -> 247.6), so dX,
+// dW and the one-launch backward keep the direct stores.
+C3_GEMM_BF16_D_KINDS_S(d256w8, 2, 4, 64, 2, 256, true)
 // d128w4: 128x128 tiles, 4 waves of 64x64, 64-deep k, 2 stages (64 KiB LDS,
 // two blocks per CU): four times the blocks of d256w8 for grids too small to
 // fill the chip with 256x256 tiles.
