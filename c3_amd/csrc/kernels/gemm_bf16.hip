@@ -1073,10 +1073,13 @@ C3_GEMM_BF16_D_KINDS_S(d256w8, 2, 4, 64, 2, 256, true)
 // d128w4: 128x128 tiles, 4 waves of 64x64, 64-deep k, 2 stages (64 KiB LDS,
 // two blocks per CU): four times the blocks of d256w8 for grids too small to
 // fill the chip with 256x256 tiles.
-C3_GEMM_BF16_D_KINDS(d128w4, 2, 2, 64, 2, 128)
+// Forwards store through LDS as d256w8's do (timed against direct stores:
+// 1024x1024x4096 18.2 -> 17.4 us, 4096x1024x1024 18.1 -> 17.1, 1024x4096x4096
+// (4 stages) 47.6 -> 46.5; k = 8192 even).
+C3_GEMM_BF16_D_KINDS_S(d128w4, 2, 2, 64, 2, 128, true)
 // d128w4s4: the same tiles with 4 stages (128 KiB, one block per CU, three
 // tiles in flight) for grids of one block per CU over long k.
-C3_GEMM_BF16_D_KINDS(d128w4s4, 2, 2, 64, 4, 128)
+C3_GEMM_BF16_D_KINDS_S(d128w4s4, 2, 2, 64, 4, 128, true)
 // d64w4: 64x64 tiles, 4 waves of 32x32, 64-deep k, 4 stages (64 KiB): grids
 // of 1024x1024 outputs, where 128x128 tiles leave three quarters of the CUs
 // idle and a 2-stage pipeline exposes the memory latency at every k-tile.
