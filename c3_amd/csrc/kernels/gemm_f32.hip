@@ -231,8 +231,13 @@ __device__ __forceinline__ void f32_tile_epilogue(const GemmArgs& p, f32x16 (&ac
 // k-tiles kt with kt % (column tiles) == tn of its rows, so every k-tile of
 // every row tile is written once and the writes are spread evenly over the
 // blocks; each is written from the registers that stage it into LDS.
+// KALL > 0: every k-tile at once (the host launches these kernels only when
+// K <= 16 * KALL): all tiles' loads are issued together into registers, each
+// tile stored to its own LDS stage and one barrier taken, so the k range
+// costs one memory round trip instead of one per k-tile; the multiplies, the
+// db sums and the dZ writes are those of the loop, in the same order.
 template <int BM, int BN, int WAVES_M, int WAVES_N, bool AK, bool BKC, bool AMASK, bool BMASK,
-          bool DB, bool VEC, bool DZ = false>
+          bool DB, bool VEC, bool DZ = false, int KALL = 0>
 __device__ __forceinline__ void gemm_f32_body(const GemmArgs& p, int bid) {
     constexpr int NT = 64 * WAVES_M * WAVES_N;
     constexpr int TM = BM / WAVES_M, TN = BN / WAVES_N;
@@ -241,7 +246,7 @@ __device__ __forceinline__ void gemm_f32_body(const GemmArgs& p, int bid) {
     constexpr int STAGE = A_SIZE + B_SIZE;
     static_assert(FM >= 1 && FN >= 1 && TM % 32 == 0 && TN % 32 == 0, "wave tile of 32x32 blocks");
 
-    __shared__ __attribute__((aligned(16))) float smem[2 * STAGE];
+    __shared__ __attribute__((aligned(16))) float smem[(KALL > 0 ? KALL : 2) * STAGE];
     __shared__ float db_part[DB ? NT : 1];
 
     const int tid = threadIdx.x;
@@ -283,6 +288,64 @@ __device__ __forceinline__ void gemm_f32_body(const GemmArgs& p, int bid) {
     const int nk = (int)((p.K + kBK - 1) / kBK);
     float* __restrict__ Dz = (float*)p.dz;
     const int nbn = (int)((p.N + BN - 1) / BN);
+
+    // One k-tile's multiplies from its LDS stage, and the db sums over it.
+    auto multiply = [&](const float* As, const float* Bs) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            // Two half-steps of 4 k-values keep fewer fragment registers live.
+            float af[FM][4], bf[FN][4];
+#pragma unroll
+            for (int i = 0; i < FM; ++i) read_frag<BM, AK>(As, wm * TM + 32 * i, lane, h, af[i]);
+#pragma unroll
+            for (int j = 0; j < FN; ++j) read_frag<BN, BKC>(Bs, wn * TN + 32 * j, lane, h, bf[j]);
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][s], bf[j][s], acc[i][j], 0, 0, 0);
+        }
+        if (DB && do_db) {
+            // B tile is stored [k][n] (!BKC): thread -> column tid % BN.
+            static_assert(!DB || !BKC, "db side output needs the [k][n] B tile");
+            static_assert(!DB || NT % BN == 0, "threads per column");
+            constexpr int RPT = NT / BN;
+            const int c = tid % BN, rs = tid / BN;
+#pragma unroll
+            for (int k = rs; k < kBK; k += RPT) dbacc += Bs[k * Lds<BN, false>::STRIDE + c];
+        }
+    };
+
+    if constexpr (KALL > 0) {
+        TileLoader<BM, NT, AK, AMASK, VEC> las[KALL];
+        TileLoader<BN, NT, BKC, BMASK, VEC> lbs[KALL];
+#pragma unroll
+        for (int t = 0; t < KALL; ++t) {
+            las[t] = la;
+            lbs[t] = lb;
+            if (t < nk) {
+                const int64_t ao = (int64_t)t * a_kstep, bo = (int64_t)t * b_kstep;
+                las[t].load(A + ao, AMASK ? Am + ao : Am, lda, a_rows, p.K - (int64_t)t * kBK);
+                lbs[t].load(B + bo, BMASK ? Bm + bo : Bm, ldb, b_rows, p.K - (int64_t)t * kBK);
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < KALL; ++t) {
+            if (t < nk) {
+                if (DZ && t % nbn == tn)
+                    las[t].store_global(Dz + (int64_t)t * a_kstep, a_rows, p.K - (int64_t)t * kBK);
+                las[t].store(smem + t * STAGE);
+                lbs[t].store(smem + t * STAGE + A_SIZE);
+            }
+        }
+        __syncthreads();
+        for (int kt = 0; kt < nk; ++kt) multiply(smem + kt * STAGE, smem + kt * STAGE + A_SIZE);
+        f32_tile_epilogue<BM, BN, WAVES_M, WAVES_N, DB>(p, acc, m0, n0, wm, wn, tid, lane, do_db, dbacc, db_part);
+        return;
+    }
+
     la.load(A, Am, lda, a_rows, p.K);
     lb.load(B, Bm, ldb, b_rows, p.K);
     if (DZ && tn == 0) la.store_global(Dz, a_rows, p.K);
@@ -302,32 +365,7 @@ __device__ __forceinline__ void gemm_f32_body(const GemmArgs& p, int bid) {
             lb.load(B + bo, BMASK ? Bm + bo : Bm, ldb, b_rows, p.K - k0);
         }
 
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            // Two half-steps of 4 k-values keep fewer fragment registers live.
-            float af[FM][4], bf[FN][4];
-#pragma unroll
-            for (int i = 0; i < FM; ++i) read_frag<BM, AK>(As, wm * TM + 32 * i, lane, h, af[i]);
-#pragma unroll
-            for (int j = 0; j < FN; ++j) read_frag<BN, BKC>(Bs, wn * TN + 32 * j, lane, h, bf[j]);
-#pragma unroll
-            for (int s = 0; s < 4; ++s)
-#pragma unroll
-                for (int i = 0; i < FM; ++i)
-#pragma unroll
-                    for (int j = 0; j < FN; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][s], bf[j][s], acc[i][j], 0, 0, 0);
-        }
-
-        if (DB && do_db) {
-            // B tile is stored [k][n] (!BKC): thread -> column tid % BN.
-            static_assert(!DB || !BKC, "db side output needs the [k][n] B tile");
-            static_assert(!DB || NT % BN == 0, "threads per column");
-            constexpr int RPT = NT / BN;
-            const int c = tid % BN, rs = tid / BN;
-#pragma unroll
-            for (int k = rs; k < kBK; k += RPT) dbacc += Bs[k * Lds<BN, false>::STRIDE + c];
-        }
+        multiply(As, Bs);
 
         if (more) {
             float* Ns = smem + (cur ^ 1) * STAGE;
@@ -368,13 +406,15 @@ __device__ __forceinline__ GemmArgs split_args_f32(const GemmArgs& p) {
 // One extern "C" symbol per (layout, fusion, tile, vector) case.
 // Tile suffix _tBMxBN_wWMxWN; _v: vectorised operand loads (contiguous extent
 // % 4 == 0 and 16-byte aligned bases), _s: scalar loads.
-#define C3_GEMM_F32_ONE_DZ(NAME, BM, BN, WM, WN, OCC, AK, BKC, AMASK, BMASK, DB, DZ)                              \
-    extern "C" __global__ __launch_bounds__(64 * WM * WN, OCC) void NAME##_v(GemmArgs p) {                         \
-        gemm_f32_body<BM, BN, WM, WN, AK, BKC, AMASK, BMASK, DB, true, DZ>(split_args_f32<AK, BKC>(p), blockIdx.x);  \
-    }                                                                                                             \
-    extern "C" __global__ __launch_bounds__(64 * WM * WN, OCC) void NAME##_s(GemmArgs p) {                         \
-        gemm_f32_body<BM, BN, WM, WN, AK, BKC, AMASK, BMASK, DB, false, DZ>(split_args_f32<AK, BKC>(p), blockIdx.x); \
+#define C3_GEMM_F32_ONE_DZK(NAME, BM, BN, WM, WN, OCC, AK, BKC, AMASK, BMASK, DB, DZ, KA)                                 \
+    extern "C" __global__ __launch_bounds__(64 * WM * WN, OCC) void NAME##_v(GemmArgs p) {                               \
+        gemm_f32_body<BM, BN, WM, WN, AK, BKC, AMASK, BMASK, DB, true, DZ, KA>(split_args_f32<AK, BKC>(p), blockIdx.x);  \
+    }                                                                                                                   \
+    extern "C" __global__ __launch_bounds__(64 * WM * WN, OCC) void NAME##_s(GemmArgs p) {                               \
+        gemm_f32_body<BM, BN, WM, WN, AK, BKC, AMASK, BMASK, DB, false, DZ, KA>(split_args_f32<AK, BKC>(p), blockIdx.x); \
     }
+#define C3_GEMM_F32_ONE_DZ(NAME, BM, BN, WM, WN, OCC, AK, BKC, AMASK, BMASK, DB, DZ) \
+    C3_GEMM_F32_ONE_DZK(NAME, BM, BN, WM, WN, OCC, AK, BKC, AMASK, BMASK, DB, DZ, 0)
 #define C3_GEMM_F32_ONE(NAME, BM, BN, WM, WN, OCC, AK, BKC, AMASK, BMASK, DB) \
     C3_GEMM_F32_ONE_DZ(NAME, BM, BN, WM, WN, OCC, AK, BKC, AMASK, BMASK, DB, false)
 
@@ -391,6 +431,23 @@ __device__ __forceinline__ GemmArgs split_args_f32(const GemmArgs& p) {
     C3_GEMM_F32_ONE(c3_gemm_f32_tt_##T, BM, BN, WM, WN, OCC, false, true, false, false, false)
 
 C3_GEMM_F32_KINDS(t64x64, 64, 64, 2, 2, 2)
+// t64x64k: the 64x64 kinds with every k-tile loaded at once, for K <= 128
+// (eight 16-deep k-tiles, eight LDS stages), vector-aligned operands only
+// (the scalar-load form measured slower: its many predicated loads and
+// larger code cost more than the round trips they save).
+#define C3_GEMM_F32_ONE_VK(NAME, BM, BN, WM, WN, OCC, AK, BKC, AMASK, BMASK, DB, DZ, KA)                                 \
+    extern "C" __global__ __launch_bounds__(64 * WM * WN, OCC) void NAME##_v(GemmArgs p) {                               \
+        gemm_f32_body<BM, BN, WM, WN, AK, BKC, AMASK, BMASK, DB, true, DZ, KA>(split_args_f32<AK, BKC>(p), blockIdx.x);  \
+    }
+#define C3_GEMM_F32_KINDS_KALL(T, BM, BN, WM, WN, OCC, KA)                                                         \
+    C3_GEMM_F32_ONE_VK(c3_gemm_f32_fwd_##T, BM, BN, WM, WN, OCC, true, false, false, false, false, false, KA)      \
+    C3_GEMM_F32_ONE_VK(c3_gemm_f32_dx_##T, BM, BN, WM, WN, OCC, true, true, false, false, false, false, KA)        \
+    C3_GEMM_F32_ONE_VK(c3_gemm_f32_dx_mask_##T, BM, BN, WM, WN, OCC, true, true, true, false, false, false, KA)    \
+    C3_GEMM_F32_ONE_VK(c3_gemm_f32_dx_mask_dz_##T, BM, BN, WM, WN, OCC, true, true, true, false, false, true, KA)  \
+    C3_GEMM_F32_ONE_VK(c3_gemm_f32_dw_##T, BM, BN, WM, WN, OCC, false, false, false, false, true, false, KA)       \
+    C3_GEMM_F32_ONE_VK(c3_gemm_f32_dw_mask_##T, BM, BN, WM, WN, OCC, false, false, false, true, true, false, KA)   \
+    C3_GEMM_F32_ONE_VK(c3_gemm_f32_tt_##T, BM, BN, WM, WN, OCC, false, true, false, false, false, false, KA)
+C3_GEMM_F32_KINDS_KALL(t64x64k, 64, 64, 2, 2, 2, 8)
 C3_GEMM_F32_KINDS(t128x128, 128, 128, 2, 2, 2)
 C3_GEMM_F32_KINDS(t256x128, 256, 128, 4, 2, 1)
 C3_GEMM_F32_KINDS(t128x256, 128, 256, 2, 4, 1)
@@ -407,19 +464,23 @@ struct BwdPairArgs {
     int _pad;
 };
 
-#define C3_GEMM_F32_BWD_PAIR(NAME, BM, BN, WM, WN, OCC, MASK, VEC)                                              \
+#define C3_GEMM_F32_BWD_PAIR_K(NAME, BM, BN, WM, WN, OCC, MASK, VEC, KA)                                        \
     extern "C" __global__ __launch_bounds__(64 * WM * WN, OCC) void NAME(BwdPairArgs p) {                      \
         const int b = blockIdx.x;                                                                              \
         if (b < p.nx)                                                                                          \
-            gemm_f32_body<BM, BN, WM, WN, true, true, MASK, false, false, VEC>(p.dx, b);                      \
+            gemm_f32_body<BM, BN, WM, WN, true, true, MASK, false, false, VEC, false, KA>(p.dx, b);           \
         else                                                                                                   \
-            gemm_f32_body<BM, BN, WM, WN, false, false, false, MASK, true, VEC>(p.dw, b - p.nx);              \
+            gemm_f32_body<BM, BN, WM, WN, false, false, false, MASK, true, VEC, false, KA>(p.dw, b - p.nx);   \
     }
+#define C3_GEMM_F32_BWD_PAIR(NAME, BM, BN, WM, WN, OCC, MASK, VEC) C3_GEMM_F32_BWD_PAIR_K(NAME, BM, BN, WM, WN, OCC, MASK, VEC, 0)
 
 C3_GEMM_F32_BWD_PAIR(c3_gemm_f32_bwd_t64x64_v, 64, 64, 2, 2, 2, false, true)
 C3_GEMM_F32_BWD_PAIR(c3_gemm_f32_bwd_t64x64_s, 64, 64, 2, 2, 2, false, false)
 C3_GEMM_F32_BWD_PAIR(c3_gemm_f32_bwd_mask_t64x64_v, 64, 64, 2, 2, 2, true, true)
 C3_GEMM_F32_BWD_PAIR(c3_gemm_f32_bwd_mask_t64x64_s, 64, 64, 2, 2, 2, true, false)
+// Both GEMMs with k <= 128, vector-aligned: every k-tile at once.
+C3_GEMM_F32_BWD_PAIR_K(c3_gemm_f32_bwd_t64x64k_v, 64, 64, 2, 2, 2, false, true, 8)
+C3_GEMM_F32_BWD_PAIR_K(c3_gemm_f32_bwd_mask_t64x64k_v, 64, 64, 2, 2, 2, true, true, 8)
 
 // ===========================================================================
 // Direct-to-LDS fp32 kernels (tiles t256x128d, t128x256d): the operand tiles go from global

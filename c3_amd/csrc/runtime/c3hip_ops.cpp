@@ -407,6 +407,17 @@ bool vec_ok(bool kc, int64_t rows, int64_t k, int64_t ld, const void* p, const v
 // fewer than 32 tiles with K >= 512 and no db side output splits k into
 // 16-aligned parts at least 128 deep, up to 256 blocks; 0 = no split.  A
 // forced tile never splits.
+// Kernel name of register tile t for a GEMM over K: the 64x64 tile's
+// all-k-at-once kernels (t64x64k: every k-tile's loads issued together, one
+// memory round trip) for K <= 128 with vector-aligned operands, else the
+// tile's k loop.  Same operations in the same order, so the same bits.
+// Measured on MI355X in the 784-256-128-10 train step: layer 2's one-launch
+// backward 11.6 -> 10.6 us, layer 1's dW 11.4 -> 10.4; the scalar-load
+// kernels (layer 3, N = 10) were slower in that form and keep the loop.
+const char* f32_reg_name(const Tile* t, int64_t K, bool vec) {
+    return t == &kF32Tiles[0] && K <= 128 && vec ? "t64x64k" : t->name;
+}
+
 int plan_split_f32(const GemmArgs& a, const Tile* t) {
     if (!t_tile_f32.empty() || std::getenv("C3_HIP_GEMM_TILE")) return 0;
     if (t->bm != 64 || a.db != nullptr || a.dz != nullptr || a.K < 512) return 0;
@@ -435,7 +446,7 @@ int run_split_f32(Kind kind, const GemmArgs& a0, const Tile* t, int S, bool vec,
     g.c_split = slice;
     char name[96];
     if (t->bk) std::snprintf(name, sizeof(name), "c3_gemm_f32_%s_%s", kind_name(kind), t->name);
-    else std::snprintf(name, sizeof(name), "c3_gemm_f32_%s_%s_%s", kind_name(kind), t->name, vec ? "v" : "s");
+    else std::snprintf(name, sizeof(name), "c3_gemm_f32_%s_%s_%s", kind_name(kind), f32_reg_name(t, split_k, vec), vec ? "v" : "s");
     void* args[] = {&g};
     rc = launch(name, dim3((unsigned)tile_count(a0, t), (unsigned)S), dim3(t->threads), args, stream);
     if (rc == C3HIP_OK) {
@@ -508,7 +519,7 @@ int run_gemm(int dtype, Kind kind, const GemmArgs& a0, bool a_kc, bool b_kc, hip
     t = f32_register_twin(t);
     if (const int S = plan_split_f32(a, t)) return run_split_f32(kind, a, t, S, vec, stream, ws);
     char name[96];
-    std::snprintf(name, sizeof(name), "c3_gemm_f32_%s_%s_%s", kind_name(kind), t->name, vec ? "v" : "s");
+    std::snprintf(name, sizeof(name), "c3_gemm_f32_%s_%s_%s", kind_name(kind), f32_reg_name(t, a.K, vec), vec ? "v" : "s");
     const int64_t blocks = ((a.M + t->bm - 1) / t->bm) * ((a.N + t->bn - 1) / t->bn);
     if (blocks > 0x7fffffff) return set_error(C3HIP_ERR_TOO_LARGE, "GEMM grid too large");
     void* args[] = {&a};
@@ -951,7 +962,8 @@ int linear_bwd_pair(const GemmArgs& ax, const GemmArgs& aw, bool relu, hipStream
     p.dw = aw;
     p.nx = (int)nx;
     char name[64];
-    std::snprintf(name, sizeof(name), "c3_gemm_f32_bwd%s_t64x64_%s", relu ? "_mask" : "", vec ? "v" : "s");
+    std::snprintf(name, sizeof(name), "c3_gemm_f32_bwd%s_%s_%s", relu ? "_mask" : "",
+                  ax.K <= 128 && aw.K <= 128 && vec ? "t64x64k" : "t64x64", vec ? "v" : "s");
     void* args[] = {&p};
     return launch(name, dim3((unsigned)(nx + nw)), dim3(t->threads), args, stream);
 }

@@ -56,8 +56,11 @@ def test_code_objects_hold_every_dispatched_kernel():
         for tile in ["t256x128d", "t128x256d", "t64x64d"]:
             assert f"c3_gemm_f32_{kind}_{tile}" in gemm
     assert {"c3_gemm_f32_dx_t256x256d", "c3_gemm_f32_dw_t256x256d"} <= gemm
+    for kind in ["fwd", "dx", "dx_mask", "dx_mask_dz", "dw", "dw_mask", "tt"]:  # every k-tile at once (k <= 128)
+        assert f"c3_gemm_f32_{kind}_t64x64k_v" in gemm
     for name in ["c3_gemm_f32_bwd_t64x64", "c3_gemm_f32_bwd_mask_t64x64"]:
         assert f"{name}_v" in gemm and f"{name}_s" in gemm
+    assert {"c3_gemm_f32_bwd_t64x64k_v", "c3_gemm_f32_bwd_mask_t64x64k_v"} <= gemm
     bf = _kernel_symbols(LIB / "gemm_bf16.hsaco")
     for tile in ["d256w8", "d256rq", "d256pp", "d128w4", "d128w4s4", "d64w4"]:
         for kind in ["fwd", "dx", "dw", "dwb", "tt", "fwdt", "fwdf", "dxf", "ttf"]:

@@ -154,6 +154,43 @@ def _run_bwd(stream, X, W, Y, dY, act, want=("dX", "dW", "db")):
     return (None if dX is None else host(dX), None if dW is None else host(dW), None if db is None else host(db))
 
 
+def test_f32_all_k_at_once_kernels_match_the_k_loop(gpu, stream):
+    # GEMMs over k <= 128 on the 64x64 register tile with vector-aligned
+    # operands issue every k-tile's loads at once (t64x64k kernels); k = 144
+    # takes the k loop.  Padding k from 128 to 144 with zero operands (an
+    # exact +-0 added to each sum) must leave the real-valued outputs
+    # unchanged bit for bit: the forward (289 tiles of 64x64, more than the
+    # direct 64x64 tile takes) and the one-launch ReLU backward (dX over
+    # k = N, dW over k = M, db).
+    rng = np.random.default_rng(0x64)
+    M, K, Nn = 1088, 128, 1088
+    X = rng.standard_normal((M, K + 16), dtype=np.float32)
+    X[:, K:] = 0.0
+    W = rng.standard_normal((K + 16, Nn), dtype=np.float32) / np.float32(12.0)
+    b = rng.standard_normal(Nn, dtype=np.float32)
+    outs = []
+    for k in (K, K + 16):
+        Yg = empty((M, Nn))
+        N.linear_fwd(N.F32, ptr(dev(np.ascontiguousarray(X[:, :k]))), ptr(dev(np.ascontiguousarray(W[:k]))), ptr(dev(b)),
+                     ptr(Yg), M, k, Nn, 1, stream)
+        outs.append(host(Yg))
+    same_bits(outs[0], outs[1])
+
+    M, K, Nn = 128, 96, 128
+    X = rng.standard_normal((M + 16, K), dtype=np.float32)
+    W = rng.standard_normal((K, Nn + 16), dtype=np.float32) / np.float32(10.0)
+    Y = rng.standard_normal((M + 16, Nn + 16), dtype=np.float32)
+    dY = rng.standard_normal((M + 16, Nn + 16), dtype=np.float32)
+    dY[M:, :] = 0.0
+    dY[:, Nn:] = 0.0
+    gX, gW, gb = _run_bwd(stream, X[:M], np.ascontiguousarray(W[:, :Nn]), np.ascontiguousarray(Y[:M, :Nn]),
+                          np.ascontiguousarray(dY[:M, :Nn]), 1)
+    pX, pW, pb = _run_bwd(stream, X, W, Y, dY, 1)
+    same_bits(gX, pX[:M])
+    same_bits(gW, pW[:, :Nn])
+    same_bits(gb, pb[:Nn])
+
+
 @pytest.mark.parametrize("M,K,Nn,act", [(128, 256, 128, 1), (128, 128, 10, 0), (37, 70, 33, 1), (64, 300, 40, 1),
                                           (200, 96, 130, 0)])
 def test_small_bwd_one_launch_matches_two(gpu, stream, monkeypatch, M, K, Nn, act):
