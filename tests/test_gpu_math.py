@@ -147,8 +147,13 @@ def test_linear_sigmoid_tanh_fp32(gpu, stream, act, M, K, Nn):
     assert_close_gemm(host(db), rb, 2.02 * M * U * np.abs(dZ.astype(np.float64)).sum(0), FP32_TOL, what="db")
 
 
+# tile: the size heuristic's kernels, or a forced direct tile, whose forward
+# stores whole tiles through LDS (the sigmoid and tanh epilogues on that path).
+@pytest.mark.parametrize("tile", [None, "d256w8", "d128w4s4"])
 @pytest.mark.parametrize("act", [N.ACT_SIGMOID, N.ACT_TANH])
-def test_linear_sigmoid_tanh_bf16(gpu, stream, act):
+def test_linear_sigmoid_tanh_bf16(gpu, stream, monkeypatch, act, tile):
+    if tile:
+        monkeypatch.setenv("C3_HIP_GEMM_TILE_BF16", tile)
     M, K, Nn = 512, 256, 264
     X = O.round_bf16(O.normal(630, (M, K)))
     W = O.round_bf16(O.normal(631, (K, Nn), 0.0, 1.0 / np.sqrt(K)))
