@@ -308,8 +308,10 @@ C3_GEMM_BF16_KINDS(t256x256, 256, 256, 2, 2)
 // so "tile kt has landed" is s_waitcnt vmcnt(<instructions issued after it>);
 // the barrier that follows makes every wave's part of tile kt visible and
 // ends every read of the stage that is refilled next.
-// Requires K % BK == 0 and the contiguous extents % 8 == 0 (host-checked);
-// rows past M or N are loaded from a clamped address and never stored.
+// Requires the contiguous extents % 8 == 0 (host-checked); K % BK == 0 for
+// the ping-pong and 4-wave kernels, any K for the others (a partial last
+// k-tile, DirectTile::issue_partial); rows past M or N are loaded from a
+// clamped address and never stored.
 // ===========================================================================
 namespace {
 
