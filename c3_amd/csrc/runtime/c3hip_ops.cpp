@@ -641,6 +641,15 @@ struct Bf16BwdArgs {
 // process over the 27 sweep shapes (bit-identical outputs): 1024^3
 // backward 24.5 -> 19.5 us, 1024x4096x1024 44.2 -> 33.4, 4096^3 270 -> 262;
 // the others within 1%.
+// Where the heuristic puts dX and dW on different 128x128 / 256x256 tiles,
+// both run on the two-stage 128x128 tile in one launch (two blocks per CU),
+// up to 4608 such tiles in all (the largest pair measured; larger pairs keep
+// the separate launches).  Measured alternately against the separate
+// launches (backward with its pre-pass, bit-identical): 1024x4096x4096
+// 107.4 -> 90.2 us, 1024x4096x8192 189.2 -> 158.4, 1024x8192x4096 166.0 ->
+// 151.7, 1024x8192x8192 336.1 -> 323.6, 4096x1024x8192 189.5 -> 168.1,
+// 4096x4096x1024 100.9 -> 94.7, 4096x8192x1024 159.5 -> 159.2; the
+// four-stage 128x128 tile for both was slower than the separate launches.
 bool bf16_bwd_pair_tiles(const GemmArgs& ax, const GemmArgs& aw, const Tile** tx, const Tile** tw) {
     if (bf16_forced()) return false;
     if (!bf16_vec_ok(true, ax.M, ax.K, ax.lda, ax.A, nullptr) || !bf16_vec_ok(true, ax.N, ax.K, ax.ldb, ax.B, nullptr) ||
@@ -654,7 +663,15 @@ bool bf16_bwd_pair_tiles(const GemmArgs& ax, const GemmArgs& aw, const Tile** tx
     auto is = [](const Tile* t, const char* n) { return std::strcmp(t->name, n) == 0; };
     const bool same = *tx == *tw && (is(*tx, "d256w8") || is(*tx, "d128w4") || is(*tx, "d128w4s4") || is(*tx, "d64w4"));
     const bool mixed = (is(*tx, "d64w4") && is(*tw, "d128w4")) || (is(*tx, "d128w4") && is(*tw, "d64w4"));
-    if (!same && !mixed) return false;
+    if (!same && !mixed) {
+        auto direct = [&](const Tile* t) { return is(t, "d256w8") || is(t, "d128w4") || is(t, "d128w4s4"); };
+        if (!direct(*tx) || !direct(*tw)) return false;
+        // choose_bf16_direct returned a direct tile for each, so both passed
+        // k_ok for the 128x128 tile too.
+        const Tile* t = find_tile(kBf16Direct, sizeof(kBf16Direct) / sizeof(kBf16Direct[0]), "d128w4");
+        if (!t || tile_count(ax, t) + tile_count(aw, t) > 4608) return false;
+        *tx = *tw = t;
+    }
     return tile_count(ax, *tx) + tile_count(aw, *tw) + (aw.N + 63) / 64 <= 0x7fffffff;
 }
 

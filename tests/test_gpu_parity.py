@@ -642,15 +642,17 @@ def test_bf16_split_k_bit_exact(gpu, stream, monkeypatch, tile, M, K, Nn):
 # column-sum launches on it (no split on these shapes either) must give the
 # same bits on real-valued inputs (every direct tile adds k in the same
 # order).  One shape per one-launch kernel, with each activation's pre-pass
-# on the smallest, and partial last k-tiles in dX (k = N = 1000) and dW
-# (k = M = 1000).
+# on the smallest, partial last k-tiles in dX (k = N = 1000) and dW
+# (k = M = 1000), and two shapes whose dX and dW the heuristic alone would
+# put on different 128x128 / 256x256 tiles (both run on d128w4 instead).
 @pytest.mark.parametrize("M,K,Nn,pair,tile,act", [
     (1000, 1016, 1024, "d64w4", "d64w4", 1), (1000, 1016, 1024, "d64w4", "d64w4", 2),
     (1000, 1016, 1024, "d64w4", "d64w4", 3), (1000, 1016, 1024, "d64w4", "d64w4", 0),
     (1024, 4096, 1024, "d128w4", "d128w4", 1), (2048, 2048, 2048, "d128w4s4", "d128w4s4", 1),
     (4096, 4096, 4096, "d256w8", "d256w8", 1), (1024, 1024, 4096, "d64w4_d128w4", "d64w4", 1),
     (4096, 1024, 1024, "d128w4_d64w4", "d64w4", 1), (1024, 1024, 1000, "d64w4", "d64w4", 1),
-    (1000, 1016, 1000, "d64w4", "d64w4", 3)])
+    (1000, 1016, 1000, "d64w4", "d64w4", 3), (1024, 4096, 4096, "d128w4", "d128w4", 1),
+    (4096, 1024, 8192, "d128w4", "d128w4", 1)])
 def test_bf16_layer_backward_one_launch_matches_separate(gpu, stream, M, K, Nn, pair, tile, act):
     from tests.parity import dev_bf16
 
