@@ -137,6 +137,9 @@ __device__ __forceinline__ u32x4 mask_mul8(u32x4 y, u32x4 d) {
 // into four interleaved sums (chunks c, c + 8, c + 16, c + 24 per step of
 // 32), and the eight wave sums are added in wave order.  A block of NW waves
 // runs 8 / NW virtual waves per wave, so every NW gives the same bits.
+// Eight steps of 32 issue their 32 loads before the first add (the same adds
+// in the same order): the loads of one step alone left each wave waiting a
+// full memory latency per four loads.
 // red: 8 x 64 floats of LDS.
 template <int NW>
 __device__ __forceinline__ void colsum_final_block(const float* __restrict__ part, float* __restrict__ out,
@@ -150,6 +153,18 @@ __device__ __forceinline__ void colsum_final_block(const float* __restrict__ par
         float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
         if (j < N) {
             int64_t c = w;
+            for (; c + 248 < nchunks; c += 256) {
+                float v[32];
+#pragma unroll
+                for (int u = 0; u < 32; ++u) v[u] = part[(c + 8 * u) * N + j];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    s0 += v[4 * u];
+                    s1 += v[4 * u + 1];
+                    s2 += v[4 * u + 2];
+                    s3 += v[4 * u + 3];
+                }
+            }
             for (; c + 24 < nchunks; c += 32) {
                 s0 += part[c * N + j];
                 s1 += part[(c + 8) * N + j];
