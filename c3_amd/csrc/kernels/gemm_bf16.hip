@@ -1120,7 +1120,6 @@ struct Bf16BwdArgs {
 
 C3_GEMM_BF16_BWD(d256w8, 2, 4, 2, 256)
 C3_GEMM_BF16_BWD(d128w4, 2, 2, 2, 128)
-C3_GEMM_BF16_BWD(d128w4s4, 2, 2, 4, 128)
 C3_GEMM_BF16_BWD(d64w4, 2, 2, 4, 64)
 // 64x64 and 128x128 tiles: 4 waves and 64 KiB of LDS stages each.
 C3_GEMM_BF16_BWD2(c3_gemm_bf16_bwd_d64w4_d128w4, 2, 2, 4, 64, 2, 2, 2, 128)

@@ -642,14 +642,17 @@ struct Bf16BwdArgs {
 // backward 24.5 -> 19.5 us, 1024x4096x1024 44.2 -> 33.4, 4096^3 270 -> 262;
 // the others within 1%.
 // Where the heuristic puts dX and dW on different 128x128 / 256x256 tiles,
-// both run on the two-stage 128x128 tile in one launch (two blocks per CU),
-// up to 4608 such tiles in all (the largest pair measured; larger pairs keep
-// the separate launches).  Measured alternately against the separate
-// launches (backward with its pre-pass, bit-identical): 1024x4096x4096
-// 107.4 -> 90.2 us, 1024x4096x8192 189.2 -> 158.4, 1024x8192x4096 166.0 ->
-// 151.7, 1024x8192x8192 336.1 -> 323.6, 4096x1024x8192 189.5 -> 168.1,
-// 4096x4096x1024 100.9 -> 94.7, 4096x8192x1024 159.5 -> 159.2; the
-// four-stage 128x128 tile for both was slower than the separate launches.
+// or both on the four-stage 128x128 tile, both run on the two-stage 128x128
+// tile in one launch (two blocks per CU), up to 4608 such tiles in all (the
+// largest pair measured; larger pairs keep the separate launches).
+// Measured alternately against the separate launches (backward with its
+// pre-pass, bit-identical): 1024x4096x4096 107.4 -> 90.2 us, 1024x4096x8192
+// 189.2 -> 158.4, 1024x8192x4096 166.0 -> 151.7, 1024x8192x8192 336.1 ->
+// 323.6, 4096x1024x8192 189.5 -> 168.1, 4096x4096x1024 100.9 -> 94.7,
+// 4096x8192x1024 159.5 -> 159.2; the four-stage tile for both was slower
+// than the separate launches there.  Against the four-stage one-launch pair
+// (fwd + bwd step, four alternating rounds): 4096x1024x4096 629-722 ->
+// 740-800 TFLOP/s, 2048^3 509-599 -> 610-670.
 bool bf16_bwd_pair_tiles(const GemmArgs& ax, const GemmArgs& aw, const Tile** tx, const Tile** tw) {
     if (bf16_forced()) return false;
     if (!bf16_vec_ok(true, ax.M, ax.K, ax.lda, ax.A, nullptr) || !bf16_vec_ok(true, ax.N, ax.K, ax.ldb, ax.B, nullptr) ||
@@ -661,7 +664,7 @@ bool bf16_bwd_pair_tiles(const GemmArgs& ax, const GemmArgs& aw, const Tile** tx
     *tw = choose_bf16_direct(Kind::Dw, aw, &unsupported, &sw);
     if (!*tx || !*tw || sx != 1 || sw != 1) return false;
     auto is = [](const Tile* t, const char* n) { return std::strcmp(t->name, n) == 0; };
-    const bool same = *tx == *tw && (is(*tx, "d256w8") || is(*tx, "d128w4") || is(*tx, "d128w4s4") || is(*tx, "d64w4"));
+    const bool same = *tx == *tw && (is(*tx, "d256w8") || is(*tx, "d128w4") || is(*tx, "d64w4"));
     const bool mixed = (is(*tx, "d64w4") && is(*tw, "d128w4")) || (is(*tx, "d128w4") && is(*tw, "d64w4"));
     if (!same && !mixed) {
         auto direct = [&](const Tile* t) { return is(t, "d256w8") || is(t, "d128w4") || is(t, "d128w4s4"); };

@@ -643,12 +643,13 @@ def test_bf16_split_k_bit_exact(gpu, stream, monkeypatch, tile, M, K, Nn):
 # same bits on real-valued inputs (every direct tile adds k in the same
 # order).  One shape per one-launch kernel, with each activation's pre-pass
 # on the smallest, partial last k-tiles in dX (k = N = 1000) and dW
-# (k = M = 1000), and two shapes whose dX and dW the heuristic alone would
-# put on different 128x128 / 256x256 tiles (both run on d128w4 instead).
+# (k = M = 1000), and shapes whose dX and dW the heuristic alone would put
+# on different 128x128 / 256x256 tiles or both on d128w4s4 (both run on
+# d128w4 instead; 2048^3 compares against separate d128w4s4 launches).
 @pytest.mark.parametrize("M,K,Nn,pair,tile,act", [
     (1000, 1016, 1024, "d64w4", "d64w4", 1), (1000, 1016, 1024, "d64w4", "d64w4", 2),
     (1000, 1016, 1024, "d64w4", "d64w4", 3), (1000, 1016, 1024, "d64w4", "d64w4", 0),
-    (1024, 4096, 1024, "d128w4", "d128w4", 1), (2048, 2048, 2048, "d128w4s4", "d128w4s4", 1),
+    (1024, 4096, 1024, "d128w4", "d128w4", 1), (2048, 2048, 2048, "d128w4", "d128w4s4", 1),
     (4096, 4096, 4096, "d256w8", "d256w8", 1), (1024, 1024, 4096, "d64w4_d128w4", "d64w4", 1),
     (4096, 1024, 1024, "d128w4_d64w4", "d64w4", 1), (1024, 1024, 1000, "d64w4", "d64w4", 1),
     (1000, 1016, 1000, "d64w4", "d64w4", 3), (1024, 4096, 4096, "d128w4", "d128w4", 1),
