@@ -1146,7 +1146,9 @@ C3_GEMM_BF16_RQ_KINDS(d256rq, 64, 2)
 // Split-K reduction: C[m, n] = epilogue(sum over s of ws[s * slice + m * N + n])
 // with the splits added in order s = 0, 1, ... (deterministic).  Epilogue:
 // + bias[n] (when non-null), act, then bf16 (round to nearest even) or fp32.
-// One thread per 4 consecutive columns of a row.
+// One thread per 4 consecutive columns of a row.  With N a multiple of 4 a
+// thread issues the loads of four splits before adding them (same adds, same
+// order) and, when C's rows allow it, stores its 4 outputs as one vector.
 struct SplitReduceArgs {
     const float* ws;
     void* C;
@@ -1163,10 +1165,37 @@ extern "C" __global__ __launch_bounds__(256) void c3_splitk_reduce(SplitReduceAr
     const float* w = a.ws + m * a.N + n0;
     float x[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     if ((a.N & 3) == 0) {
-        for (int s = 0; s < a.S; ++s) {
+        int s = 0;
+        for (; s + 4 <= a.S; s += 4) {
+            f32x4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v[u] = __builtin_nontemporal_load((const f32x4*)(w + (int64_t)(s + u) * a.slice));
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) x[e] += v[u][e];
+        }
+        for (; s < a.S; ++s) {
             const f32x4 v = __builtin_nontemporal_load((const f32x4*)(w + (int64_t)s * a.slice));
 #pragma unroll
             for (int e = 0; e < 4; ++e) x[e] += v[e];
+        }
+        if ((a.ldc & 3) == 0 && ((uintptr_t)a.C & (a.out_bf16 ? 7 : 15)) == 0) {
+            float y[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                y[e] = x[e];
+                if (a.bias != nullptr) y[e] = y[e] + a.bias[n0 + e];
+                y[e] = act_apply(y[e], a.act);
+            }
+            if (a.out_bf16) {
+                const unsigned lo = f32_to_bf16_rne(y[0]) | ((unsigned)f32_to_bf16_rne(y[1]) << 16);
+                const unsigned hi = f32_to_bf16_rne(y[2]) | ((unsigned)f32_to_bf16_rne(y[3]) << 16);
+                *(uint2*)((unsigned short*)a.C + m * a.ldc + n0) = make_uint2(lo, hi);
+            } else {
+                *(f32x4*)((float*)a.C + m * a.ldc + n0) = f32x4{y[0], y[1], y[2], y[3]};
+            }
+            return;
         }
     } else {
         for (int s = 0; s < a.S; ++s)
