@@ -687,6 +687,26 @@ def test_bf16_layer_backward_one_launch_matches_separate(gpu, stream, M, K, Nn, 
         same_bits(got, ref)
 
 
+def test_bf16_layer_backward_mixed_tiles_beyond_the_pair_bound_stay_separate(gpu, stream):
+    # dX on 128x128 tiles (512) and dW on 256x256 tiles (2048): on 128x128
+    # tiles the pair would be 8704 blocks, past the 4608 the one-launch rule
+    # takes, so the GEMMs run as separate launches on their own tiles.
+    M, K, Nn = 1024, 8192, 16384
+    X, W = empty((M, K), dtype=torch.bfloat16, fill=0.0), empty((K, Nn), dtype=torch.bfloat16, fill=0.0)
+    Y, dY = empty((M, Nn), dtype=torch.bfloat16, fill=0.0), empty((M, Nn), dtype=torch.bfloat16, fill=0.0)
+    dX = empty((M, K), dtype=torch.bfloat16)
+    dW, db = empty((K, Nn)), empty(Nn)
+    N.set_launch_timing(True)
+    try:
+        N.linear_bwd(N.BF16, ptr(X), ptr(W), ptr(Y), ptr(dY), ptr(dX), ptr(dW), ptr(db), M, K, Nn, 1, stream)
+        names = [n for n, _ in N.launch_timings()]
+    finally:
+        N.set_launch_timing(False)
+    assert "c3_gemm_bf16_dx_d128w4" in names and "c3_gemm_bf16_dw_d256w8" in names, names
+    assert not any(n.startswith("c3_gemm_bf16_bwd_") for n in names), names
+    assert not host(dW).any() and not host(db).any()
+
+
 def test_bf16_split_k_real_values(gpu, stream):
     # Real-valued inputs through the split forward and split dW: the split
     # order differs from the sequential k loop only by rounding.
